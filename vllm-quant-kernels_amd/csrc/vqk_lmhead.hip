@@ -1,0 +1,647 @@
+// vqk_lmhead.hip - quantized lm_head projections for gfx950 (MI355X), all five modes.
+//
+// out[b, m] = epilogue_m( sum_k W[m, k] * X[b, k] ) for a [M, K] quantized weight that is
+// streamed from HBM exactly once per launch.  One kernel template serves every mode and
+// every batch size; the work is shaped for CDNA4 rather than for a warp-GEMV:
+//
+//  * Each wavefront owns 16-row tiles of W.  Lane l holds row (l % 16) and k-block (l / 16)
+//    of the MFMA A operand, which is exactly the 16x16xKB MFMA register layout, so the
+//    weights go from a global_load_dwordx4 straight into the matrix core (int8 and e4m3/
+//    E2M1 need no conversion; W8A16 converts int8 -> fp16 with a byte permute and one
+//    packed fp16 add).  The batch (1..32 rows) is the MFMA N dimension, zero-padded to 16;
+//    at batch 1 the matrix core is 1/16 busy, which still leaves it far faster than HBM.
+//  * Because the reduction over k is order-free, a lane may hold any k positions as long
+//    as the B operand (activations) holds the same ones.  The loads are laid out so that
+//    the four k-block lanes of a row read 64 (or 128) contiguous bytes per instruction,
+//    and the activations are staged once per workgroup in LDS in the matching "fragment"
+//    order, so each B operand is one conflict-free ds_read_b128 (or two).
+//  * MX modes use the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4: a lane's 32 k values
+//    are one 32-element MX group, so the per-lane scale operand is simply that group's
+//    E8M0 byte (weights) and the activation group's byte (from LDS).
+//  * Workgroups are persistent (a few per CU); each wave walks its tiles as one flat
+//    sequence of 128-byte-per-row chunks through a D-deep register ring, so loads for the
+//    next tile are in flight while the current tile's epilogue runs.
+//  * Runtime activation quantization (per-tensor INT8, e4m3 cast, MXFP8) runs in every
+//    workgroup's prologue while it stages X into LDS; no extra launch, no host sync.
+//
+// Reference semantics: src/vllm_quant_kernels/_kernels.py (int8_gmv :8-84, int8_gemm
+// :148-250, fp8_gemm :258-360, int8_w8a8_gemm :369-479, mxfp8_gemm :491-634, mxfp4_gemm
+// :649-804) and the activation quantization in src/vllm_quant_kernels/_quant.py (:34-61,
+// :413, :535-540).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vqk.h"
+#include "vqk_internal.h"
+#include "vqk_math.h"
+
+namespace vqk {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+enum Mode { M_W8A16 = 0, M_W8A8 = 1, M_FP8 = 2, M_MXFP8 = 3, M_MXFP4 = 4 };
+
+template <int MODE>
+struct ModeTraits;
+// MPC: MFMAs per 128-byte chunk of a row; FB: bytes of one lane's B fragment;
+// XB: LDS bytes per activation element; KPM: k values per MFMA (per row);
+// MX: has E8M0 group scales; ACC_INT: int32 accumulator.
+template <> struct ModeTraits<M_W8A16> { enum { MPC = 4, FB = 16, XB = 2, KPM = 32, MX = 0, ACC_INT = 0 }; };
+template <> struct ModeTraits<M_W8A8>  { enum { MPC = 2, FB = 16, XB = 1, KPM = 64, MX = 0, ACC_INT = 1 }; };
+template <> struct ModeTraits<M_FP8>   { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 0, ACC_INT = 0 }; };
+template <> struct ModeTraits<M_MXFP8> { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
+template <> struct ModeTraits<M_MXFP4> { enum { MPC = 2, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
+
+// k offset (within a row) of the first element of B fragment (mi, g): the k positions a
+// lane of k-block g holds for the mi-th MFMA of a row.  Must match the weight addressing
+// in load_chunk(): chunk c = bytes [128c, 128c+128) of the row.
+template <int MODE>
+__device__ __forceinline__ int frag_k0(int mi, int g) {
+  if (MODE == M_W8A16) {  // mi = 4c + 2h + q; lane bytes [128c + 64h + 16g, +16), q-th half
+    int c = mi >> 2, h = (mi >> 1) & 1, q = mi & 1;
+    return 128 * c + 64 * h + 16 * g + 8 * q;
+  } else if (MODE == M_W8A8) {  // mi = 2c + h; bytes [128c + 64h + 16g, +16)
+    int c = mi >> 1, h = mi & 1;
+    return 128 * c + 64 * h + 16 * g;
+  } else if (MODE == M_MXFP4) {  // mi = 2c + h; bytes [128c + 64h + 16g, +16) = k [256c+128h+32g, +32)
+    int c = mi >> 1, h = mi & 1;
+    return 256 * c + 128 * h + 32 * g;
+  } else {  // FP8 / MXFP8: mi = c; bytes [128c + 32g, +32)
+    return 128 * mi + 32 * g;
+  }
+}
+
+struct LmArgs {
+  const uint8_t* w;     // [M, KB] bytes
+  const void* ws;       // per-row scales (fp16 or fp32) [M] or MX scales [M, K/32]
+  const void* x;        // activations of this batch group, row stride ldx (or null)
+  int xdt;              // dtype code of x (W8A16: fp16 only)
+  const uint8_t* xq;    // pre-quantized e4m3 activations [Bg, K] (MX gemm forms) or null
+  const uint8_t* xsq;   // pre-quantized E8M0 scales [Bg, K/32] or null
+  const void* xall;     // W8A8: the whole activation tensor (amax is per-tensor)
+  int64_t ldx;
+  uint16_t* out;        // [Bg, ldo] (already offset to the group's first row)
+  int64_t ldo;
+  int32_t* acc;         // W8A8 optional [Bg, M]
+  int M, K, Bg, Ball;
+  int out_vec;          // 1 when 8-byte output stores are aligned
+  float xs_val;         // W8A8 with pre-quantized activations: the per-tensor scale
+};
+
+// ---------------------------------------------------------------------------------------
+// Prologue: stage the activations of this batch group into LDS in fragment order.
+// Fragment (mi, g, b) lives at byte ((mi*4 + g) * Bg + b) * FB; a zero fragment follows.
+// MX scales: dword ((mi/4)*4 + g) * Bg + b holds byte (mi % 4) for fragment mi.
+template <int MODE>
+__device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
+  typedef ModeTraits<MODE> T;
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int K = a.K, Bg = a.Bg;
+  const int NMF = K / T::KPM;  // MFMAs per row
+  const int nfrag = NMF * 4 * Bg;
+  uint8_t* zero = lds + (size_t)nfrag * T::FB;
+  for (int i = tid; i < T::FB / 4; i += nth) ((uint32_t*)zero)[i] = 0u;
+
+  float xs_w8a8 = a.xs_val;
+  if (MODE == M_W8A8 && !a.xq) {
+    // per-tensor amax over the whole [Ball, K] activation (bit-exact max, order-free)
+    float m = 0.f;
+    for (int b = 0; b < a.Ball; ++b)
+      for (int k = tid; k < K; k += nth) m = fmaxf(m, fabsf(load_as_f32(a.xall, a.xdt, (int64_t)b * a.ldx + k)));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) lds_red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+      float mm = 0.f;
+      for (int i = 0; i < (nth >> 6); ++i) mm = fmaxf(mm, lds_red[i]);
+      lds_red[16] = fmaxf(mm / 127.0f, 1e-12f);
+    }
+    __syncthreads();
+    xs_w8a8 = lds_red[16];
+  } else if (MODE == M_W8A8) {
+    if (tid == 0) lds_red[16] = xs_w8a8;
+  }
+
+  for (int f = tid; f < nfrag; f += nth) {
+    int b = f % Bg;
+    int gm = f / Bg;
+    int g = gm & 3, mi = gm >> 2;
+    int k0 = frag_k0<MODE>(mi, g);
+    uint8_t* dst = lds + (size_t)f * T::FB;
+    const int64_t xo = (int64_t)b * a.ldx + k0;
+    if (MODE == M_W8A16) {
+      const uint16_t* src = (const uint16_t*)a.x + xo;
+      uint32_t v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+    } else if ((MODE == M_W8A8 || MODE == M_FP8) && a.xq) {
+      // pre-quantized int8 / e4m3 activations [Bg, K]: copy the fragment's bytes
+      const uint8_t* src = a.xq + (int64_t)b * K + k0;
+#pragma unroll
+      for (int e = 0; e < T::FB; e += 4)
+        *(uint32_t*)(dst + e) = (uint32_t)src[e] | ((uint32_t)src[e + 1] << 8) | ((uint32_t)src[e + 2] << 16) |
+                                ((uint32_t)src[e + 3] << 24);
+    } else if (MODE == M_W8A8) {
+      uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float q = __builtin_rintf(load_as_f32(a.x, a.xdt, xo + e) / xs_w8a8);
+        q = fminf(fmaxf(q, -127.f), 127.f);
+        v[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * (e & 3));
+      }
+      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+    } else if (MODE == M_FP8) {
+      uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)f32_to_e4m3(load_as_f32(a.x, a.xdt, xo + e)) << (8 * (e & 3));
+      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+      *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
+    } else {  // MX: one 32-element group per fragment
+      uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      uint32_t sbyte;
+      if (a.xq) {
+        const uint8_t* src = a.xq + (int64_t)b * K + k0;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+        sbyte = a.xsq[(int64_t)b * (K / 32) + (k0 >> 5)];
+      } else {
+        float xv[32];
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+          xv[e] = load_as_f32(a.x, a.xdt, xo + e);
+          amax = fmaxf(amax, fabsf(xv[e]));
+        }
+        int kx = mx_exponent(amax, 448.0f);
+        float sc = exp2i(kx);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+          float y = fminf(fmaxf(xv[e] / sc, -448.0f), 448.0f);
+          v[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
+        }
+        sbyte = (uint32_t)(kx + 127);
+      }
+      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+      *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
+      // scale byte: gather per dword below (byte writes into LDS are fine on gfx950)
+      uint8_t* sdst = (uint8_t*)(lds_xs + ((size_t)((mi >> 2) * 4 + g) * Bg + b)) + (mi & 3);
+      *sdst = (uint8_t)sbyte;
+    }
+  }
+  if (T::MX) {
+    // padding lanes (b >= Bg) read this dword: scale 1.0 (byte 127) in every position
+    const int nsd = ((NMF + 3) / 4) * 4 * Bg;
+    if (tid == 0) lds_xs[nsd] = 0x7F7F7F7Fu;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------
+// One ring slot: the 32 weight bytes a lane owns in one 128-byte chunk of its row (plus the
+// chunk's MX scale dwords).  FP8 modes keep them as one v8i so the MFMA A operand needs no
+// register copy.
+template <int MODE>
+struct Slot {
+  v4i lo, hi;
+  uint32_t s0, s1;
+};
+template <>
+struct Slot<M_FP8> {
+  v8i w;
+  uint32_t s0, s1;
+};
+template <>
+struct Slot<M_MXFP8> {
+  v8i w;
+  uint32_t s0, s1;
+};
+
+template <int MODE>
+__device__ __forceinline__ void load_chunk(Slot<MODE>& s, const uint8_t* rowp, const uint32_t* srowp,
+                                           int c, int g) {
+  if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
+    const v4i* p = (const v4i*)(rowp + 128 * c + 32 * g);
+    v4i lo = __builtin_nontemporal_load(p);
+    v4i hi = __builtin_nontemporal_load(p + 1);
+    s.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    s.lo = __builtin_nontemporal_load((const v4i*)(rowp + 128 * c + 16 * g));
+    s.hi = __builtin_nontemporal_load((const v4i*)(rowp + 128 * c + 64 + 16 * g));
+  }
+  if (MODE == M_MXFP8) {
+    s.s0 = srowp[c];
+  } else if (MODE == M_MXFP4) {
+    s.s0 = srowp[2 * c];
+    s.s1 = srowp[2 * c + 1];
+  }
+}
+
+// int8 x4 (one dword) -> two packed fp16 pairs, exactly: (b ^ 0x80) | 0x6400 is the fp16
+// value 1152 + b, so one packed subtraction of 1152 leaves b.
+__device__ __forceinline__ void i8x4_to_h(uint32_t d, v2h& p0, v2h& p1) {
+  uint32_t u = d ^ 0x80808080u;
+  uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const v2h bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  p0 = __builtin_bit_cast(v2h, a) - bias;
+  p1 = __builtin_bit_cast(v2h, b) - bias;
+}
+
+template <int MODE>
+struct AccT {
+  typedef v4f type;
+};
+template <>
+struct AccT<M_W8A8> {
+  typedef v4i type;
+};
+template <int MODE, int NCT>
+struct Acc {
+  typename AccT<MODE>::type v[NCT];
+  __device__ __forceinline__ void zero(int ct) { v[ct] = (typename AccT<MODE>::type)(0); }
+};
+
+// B-operand LDS byte offset for MFMA mi, lane (g, j), column tile ct.
+template <int MODE>
+__device__ __forceinline__ uint32_t frag_off(int mi, int g, int b, int Bg, uint32_t zero_off) {
+  typedef ModeTraits<MODE> T;
+  return (b < Bg) ? (uint32_t)(((mi * 4 + g) * Bg + b) * T::FB) : zero_off;
+}
+
+template <int MODE, int NCT>
+__device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MODE>& s, int c, int g,
+                                              int j, int Bg, const uint8_t* lds, uint32_t zero_off,
+                                              const uint32_t* lds_xs, uint32_t xs_pad_idx) {
+  typedef ModeTraits<MODE> T;
+  if constexpr (MODE == M_W8A16) {
+    uint32_t d[8] = {(uint32_t)s.lo.x, (uint32_t)s.lo.y, (uint32_t)s.lo.z, (uint32_t)s.lo.w,
+                     (uint32_t)s.hi.x, (uint32_t)s.hi.y, (uint32_t)s.hi.z, (uint32_t)s.hi.w};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {  // m = 2h + q: dwords 2m, 2m+1
+      v2h p0, p1, p2, p3;
+      i8x4_to_h(d[2 * m], p0, p1);
+      i8x4_to_h(d[2 * m + 1], p2, p3);
+      v8h A = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+      const int mi = 4 * c + m;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        v8h Bv = *(const v8h*)(lds + frag_off<MODE>(mi, g, ct * 16 + j, Bg, zero_off));
+        acc.v[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bv, acc.v[ct], 0, 0, 0);
+      }
+    }
+  } else if constexpr (MODE == M_W8A8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i A = h ? s.hi : s.lo;
+      const int mi = 2 * c + h;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        v4i Bv = *(const v4i*)(lds + frag_off<MODE>(mi, g, ct * 16 + j, Bg, zero_off));
+        acc.v[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc.v[ct], 0, 0, 0);
+      }
+    }
+  } else if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
+    const v8i A = s.w;
+    const int mi = c;
+    int sa = 127;
+    if (MODE == M_MXFP8) sa = (int)(s.s0 >> (8 * g));
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int b = ct * 16 + j;
+      const v4i* bp = (const v4i*)(lds + frag_off<MODE>(mi, g, b, Bg, zero_off));
+      v4i b0 = bp[0], b1 = bp[1];
+      v8i Bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      int sb = 127;
+      if (MODE == M_MXFP8) {
+        uint32_t di = (b < Bg) ? (uint32_t)(((mi >> 2) * 4 + g) * Bg + b) : xs_pad_idx;
+        sb = (int)(lds_xs[di] >> (8 * (mi & 3)));
+      }
+      acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc.v[ct], 0, 0, 0, sa, 0, sb);
+    }
+  } else {  // MXFP4: two MFMAs per chunk, A = 32 E2M1 values (16 bytes) per lane
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i w = h ? s.hi : s.lo;
+      // E2M1 operands occupy 4 VGPRs; the undefined upper half lets the backend pass
+      // only those four to the MFMA.
+      v8i A = __builtin_shufflevector(w, w, 0, 1, 2, 3, -1, -1, -1, -1);
+      const int mi = 2 * c + h;
+      int sa = (int)((h ? s.s1 : s.s0) >> (8 * g));
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const int b = ct * 16 + j;
+        const v4i* bp = (const v4i*)(lds + frag_off<MODE>(mi, g, b, Bg, zero_off));
+        v4i b0 = bp[0], b1 = bp[1];
+        v8i Bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+        uint32_t di = (b < Bg) ? (uint32_t)(((mi >> 2) * 4 + g) * Bg + b) : xs_pad_idx;
+        int sb = (int)(lds_xs[di] >> (8 * (mi & 3)));
+        acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc.v[ct], 4, 0, 0, sa, 0, sb);
+      }
+    }
+  }
+}
+
+// Epilogue of one 16-row tile: lane l holds D[4*(l/16) + e][l % 16], e = 0..3, i.e. rows
+// m0 + 4*(l/16) + e of column b = ct*16 + (l % 16).
+template <int MODE, int NCT>
+__device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, int m0, int lane,
+                                         float xs_w8a8) {
+  const int g = lane >> 4, j = lane & 15;
+  const int mr = m0 + 4 * g;
+  float sc[4] = {1.f, 1.f, 1.f, 1.f};
+  if (MODE == M_W8A16 || MODE == M_FP8) {
+    const uint16_t* s = (const uint16_t*)a.ws;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sc[e] = (mr + e < a.M) ? h2f(s[mr + e]) : 0.f;
+  } else if (MODE == M_W8A8) {
+    const float* s = (const float*)a.ws;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sc[e] = (mr + e < a.M) ? s[mr + e] : 0.f;
+  }
+  const bool full = (mr + 3 < a.M);
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int b = ct * 16 + j;
+    if (b < a.Bg) {
+      uint16_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float r;
+        if (MODE == M_W8A8) {
+          r = ((float)acc.v[ct][e] * sc[e]) * xs_w8a8;
+        } else if (MODE == M_W8A16 || MODE == M_FP8) {
+          r = acc.v[ct][e] * sc[e];
+        } else {
+          r = acc.v[ct][e];
+        }
+        o[e] = f2h(r);
+      }
+      uint16_t* op = a.out + (int64_t)b * a.ldo + mr;
+      if (full && a.out_vec) {
+        *(uint2*)op = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (mr + e < a.M) op[e] = o[e];
+      }
+      if (MODE == M_W8A8) {
+        if (a.acc) {
+          int32_t* ap = a.acc + (int64_t)b * a.M + mr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (mr + e < a.M) ap[e] = acc.v[ct][e];
+        }
+      }
+    }
+    acc.zero(ct);
+  }
+}
+
+template <int MODE, int NCT, int D>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) lmhead_kernel(LmArgs a) {
+  typedef ModeTraits<MODE> T;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ float red[17];
+  const int K = a.K;
+  const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;  // weight bytes per row
+  const int NMF = K / T::KPM;
+  const int Bg = a.Bg;
+  const uint32_t frag_bytes = (uint32_t)NMF * 4 * Bg * T::FB;
+  uint8_t* lds = smem;
+  uint32_t* lds_xs = (uint32_t*)(smem + frag_bytes + T::FB);
+  const uint32_t zero_off = frag_bytes;
+  const uint32_t xs_pad_idx = (uint32_t)((NMF + 3) / 4) * 4 * Bg;
+
+  stage_x<MODE>(a, lds, lds_xs, red);
+  const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int ntiles = (a.M + 15) >> 4;
+  const int wid = blockIdx.x * nwaves + wave;
+  const int total = gridDim.x * nwaves;
+  if (wid >= ntiles) return;
+  const int my_tiles = (ntiles - 1 - wid) / total + 1;
+  const int CPR = KB >> 7;  // 128-byte chunks per row; D divides CPR (host guarantees)
+  const int nchunks = my_tiles * CPR;
+
+  auto row_ptrs = [&](int tq, const uint8_t*& rp, const uint32_t*& sp) {
+    int tile = wid + tq * total;
+    int m = tile * 16 + r;
+    m = (m < a.M) ? m : (a.M - 1);
+    rp = a.w + (int64_t)m * KB;
+    sp = T::MX ? (const uint32_t*)((const uint8_t*)a.ws + (int64_t)m * (K >> 5)) : nullptr;
+  };
+
+  Slot<MODE> ring[D];
+  {
+    const uint8_t* rp;
+    const uint32_t* sp;
+    row_ptrs(0, rp, sp);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_chunk<MODE>(ring[d], rp, sp, d, g);  // D <= CPR: all in tile 0
+  }
+  Acc<MODE, NCT> acc;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
+
+  for (int q0 = 0; q0 < nchunks; q0 += D) {
+    const int tq = q0 / CPR;        // tile ordinal of this block of D chunks
+    const int c0 = q0 - tq * CPR;   // first chunk index within the tile
+    // the chunks loaded during this block are q0 + D .. q0 + 2D - 1 (same tile or next);
+    // past the end of the wave's work the current chunks are re-read instead, so the loop
+    // body has no branches and the loads stay unconditional (a few KB of extra reads)
+    const int qn = q0 + D;
+    const bool more = qn < nchunks;
+    const int tqn = more ? qn / CPR : tq;
+    const int cn0 = more ? qn - tqn * CPR : c0;
+    const uint8_t* rpn;
+    const uint32_t* spn;
+    row_ptrs(tqn, rpn, spn);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      compute_chunk<MODE, NCT>(acc, ring[d], c0 + d, g, r, Bg, lds, zero_off, lds_xs, xs_pad_idx);
+      load_chunk<MODE>(ring[d], rpn, spn, cn0 + d, g);
+      // keep each chunk's LDS reads next to its MFMAs: hoisting them across chunks only
+      // raises register pressure (and occupancy is what hides the HBM latency here)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c0 + D == CPR) epilogue<MODE, NCT>(acc, a, (wid + tq * total) * 16, lane, xs_w8a8);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Host side
+static int pick_depth(int cpr) {
+  if (cpr % 4 == 0) return 4;
+  if (cpr % 2 == 0) return 2;
+  return 1;
+}
+
+template <int MODE, int NCT>
+static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, int threads,
+                      hipStream_t st) {
+  switch (depth) {
+#define VQK_L(DD)                                                                                    \
+  case DD:                                                                                           \
+    hipLaunchKernelGGL((lmhead_kernel<MODE, NCT, DD>), dim3(grid), dim3(threads), lds_bytes, st, a); \
+    break;
+    VQK_L(1) VQK_L(2) VQK_L(4)
+#undef VQK_L
+    default:
+      return VQK_EINVAL;
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VQK_OK : (int)e;
+}
+
+template <int MODE>
+static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xdt, int64_t ldx,
+                         const uint8_t* xq, const uint8_t* xsq, uint16_t* out, int64_t ldo,
+                         int32_t* acc, int64_t M, int64_t K, int64_t B, hipStream_t st,
+                         float xs_val = 0.f) {
+  typedef ModeTraits<MODE> T;
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!w || !ws || !out || (!x && !xq) || (xq && T::MX && !xsq)) return VQK_EINVAL;
+  if (MODE == M_W8A16 && !x) return VQK_EINVAL;
+  if (x && (xdt < VQK_F32 || xdt > VQK_BF16 || (MODE == M_W8A16 && xdt != VQK_F16))) return VQK_EINVAL;
+  if (M < 1 || K < 1 || B < 0 || (x && ldx < K) || ldo < M) return VQK_EINVAL;
+  if (B == 0) return VQK_OK;
+  const int64_t kmult = (MODE == M_MXFP4) ? 256 : 128;
+  if (K % kmult != 0 || M > (int64_t)INT32_MAX - 16 || K > (1 << 20) || B > 4096) return VQK_EUNSUPPORTED;
+  if (((uintptr_t)w & 15) != 0) return VQK_EUNSUPPORTED;
+
+  const int KB = (int)((MODE == M_MXFP4) ? K / 2 : K);
+  const int cpr = KB / 128;
+  const int depth = pick_depth(cpr);
+  const size_t lds_cap = 160 * 1024 - 1024;
+  // batch group size: up to 16*NCT rows, limited by LDS
+  const size_t per_row = (size_t)K * T::XB + (T::MX ? (size_t)K / 32 : 0);
+  int gmax = (int)((lds_cap - 64 - T::FB) / per_row);
+  if (gmax < 1) return VQK_EUNSUPPORTED;
+  const int nct_max = (MODE == M_W8A16) ? 1 : 2;
+  if (gmax > 16 * nct_max) gmax = 16 * nct_max;
+  const int ngroups = (int)((B + gmax - 1) / gmax);
+  const int gsize = (int)((B + ngroups - 1) / ngroups);  // balanced groups
+  const int ncu = vqk_cu_count();
+  const int threads = 512;
+
+  for (int64_t b0 = 0; b0 < B; b0 += gsize) {
+    const int Bg = (int)((B - b0) < gsize ? (B - b0) : gsize);
+    LmArgs a;
+    a.w = w;
+    a.ws = ws;
+    const int xes = (xdt == VQK_F32) ? 4 : 2;
+    a.x = x ? (const void*)((const char*)x + b0 * ldx * xes) : nullptr;
+    a.xdt = xdt;
+    a.xq = xq ? xq + b0 * K : nullptr;
+    a.xsq = xsq ? xsq + b0 * (K / 32) : nullptr;
+    a.xall = x;
+    a.ldx = ldx;
+    a.out = out + b0 * ldo;
+    a.ldo = ldo;
+    a.acc = acc ? acc + b0 * M : nullptr;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.Bg = Bg;
+    a.Ball = (int)B;
+    a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
+    a.xs_val = xs_val;
+    const int NMF = (int)(K / T::KPM);
+    size_t lds = (size_t)NMF * 4 * Bg * T::FB + T::FB;
+    if (T::MX) lds += ((size_t)((NMF + 3) / 4) * 4 * Bg + 1) * 4;
+    lds = (lds + 15) & ~(size_t)15;
+    const int per_cu = (lds <= 48 * 1024) ? 2 : 1;
+    const int ntiles = (int)((M + 15) / 16);
+    int grid = ncu * per_cu;
+    const int max_grid = (ntiles + (threads / 64) - 1) / (threads / 64);
+    if (grid > max_grid) grid = max_grid;
+    const int nct = (Bg + 15) / 16;
+    int rc2;
+    if constexpr (MODE == M_W8A16) {
+      rc2 = launch_nct<MODE, 1>(a, depth, lds, grid, threads, st);
+    } else {
+      rc2 = (nct == 1) ? launch_nct<MODE, 1>(a, depth, lds, grid, threads, st)
+                       : launch_nct<MODE, 2>(a, depth, lds, grid, threads, st);
+    }
+    if (rc2) return rc2;
+  }
+  return VQK_OK;
+}
+
+}  // namespace vqk
+
+using namespace vqk;
+
+extern "C" int vqk_lmhead_w8a16(const int8_t* w, const uint16_t* s_f16, const uint16_t* x_f16, int64_t ldx,
+                                uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                                vqk_stream_t stream) {
+  return lmhead_launch<M_W8A16>((const uint8_t*)w, s_f16, x_f16, VQK_F16, ldx, nullptr, nullptr, out_f16, ldo,
+                                nullptr, M, K, B, (hipStream_t)stream);
+}
+
+extern "C" int vqk_lmhead_w8a8(const int8_t* w, const float* ws_f32, const void* x, int x_dtype, int64_t ldx,
+                               uint16_t* out_f16, int64_t ldo, int32_t* acc_i32, int64_t M, int64_t K,
+                               int64_t B, vqk_stream_t stream) {
+  return lmhead_launch<M_W8A8>((const uint8_t*)w, ws_f32, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo,
+                               acc_i32, M, K, B, (hipStream_t)stream);
+}
+
+extern "C" int vqk_lmhead_fp8(const uint8_t* w, const uint16_t* s_f16, const void* x, int x_dtype, int64_t ldx,
+                              uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                              vqk_stream_t stream) {
+  return lmhead_launch<M_FP8>(w, s_f16, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B,
+                              (hipStream_t)stream);
+}
+
+extern "C" int vqk_lmhead_mxfp8(const uint8_t* w, const uint8_t* ws, const void* x, int x_dtype, int64_t ldx,
+                                uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                                vqk_stream_t stream) {
+  return lmhead_launch<M_MXFP8>(w, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B,
+                                (hipStream_t)stream);
+}
+
+extern "C" int vqk_lmhead_mxfp4(const uint8_t* w_packed, const uint8_t* ws, const void* x, int x_dtype,
+                                int64_t ldx, uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                                vqk_stream_t stream) {
+  return lmhead_launch<M_MXFP4>(w_packed, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B,
+                                (hipStream_t)stream);
+}
+
+extern "C" int vqk_gemm_mxfp8(const uint8_t* w, const uint8_t* ws, const uint8_t* xq, const uint8_t* xs,
+                              uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                              vqk_stream_t stream) {
+  if (!xq || !xs) return VQK_EINVAL;
+  return lmhead_launch<M_MXFP8>(w, ws, nullptr, VQK_F16, K, xq, xs, out_f16, ldo, nullptr, M, K, B,
+                                (hipStream_t)stream);
+}
+
+extern "C" int vqk_gemm_mxfp4(const uint8_t* w_packed, const uint8_t* ws, const uint8_t* xq,
+                              const uint8_t* xs, uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K,
+                              int64_t B, vqk_stream_t stream) {
+  if (!xq || !xs) return VQK_EINVAL;
+  return lmhead_launch<M_MXFP4>(w_packed, ws, nullptr, VQK_F16, K, xq, xs, out_f16, ldo, nullptr, M, K, B,
+                                (hipStream_t)stream);
+}
+
+extern "C" int vqk_gemm_fp8(const uint8_t* w, const uint16_t* s_f16, const uint8_t* xq, uint16_t* out_f16,
+                            int64_t ldo, int64_t M, int64_t K, int64_t B, vqk_stream_t stream) {
+  if (!xq) return VQK_EINVAL;
+  return lmhead_launch<M_FP8>(w, s_f16, nullptr, VQK_F16, K, xq, nullptr, out_f16, ldo, nullptr, M, K, B,
+                              (hipStream_t)stream);
+}
+
+extern "C" int vqk_gemm_w8a8(const int8_t* w, const float* ws_f32, const int8_t* xq, float xs, uint16_t* out_f16,
+                             int64_t ldo, int32_t* acc_i32, int64_t M, int64_t K, int64_t B, vqk_stream_t stream) {
+  if (!xq) return VQK_EINVAL;
+  return lmhead_launch<M_W8A8>((const uint8_t*)w, ws_f32, nullptr, VQK_F16, K, (const uint8_t*)xq, nullptr, out_f16,
+                               ldo, acc_i32, M, K, B, (hipStream_t)stream, xs);
+}

@@ -1,0 +1,214 @@
+// vqk_quant.hip - weight quantizers (run once per lm_head) and standalone activation
+// quantizers for gfx950.  Each reproduces the reference's torch op chain bit for bit:
+//   per-row INT8   src/vllm_quant_kernels/_quant.py:245-302
+//   per-row FP8    src/vllm_quant_kernels/_quant.py:304-325
+//   MXFP8          src/vllm_quant_kernels/_quant.py:34-61
+//   MXFP4          src/vllm_quant_kernels/_quant.py:64-105
+//   W8A8 act quant src/vllm_quant_kernels/_quant.py:535-540
+//   FP8 act cast   src/vllm_quant_kernels/_quant.py:413
+// Per-row kernels use one 256-thread workgroup per row (amax, then quantize); the MX
+// kernels use one thread per 32-element group.  These are byte-streaming kernels bound by
+// HBM, so they use plain coalesced loads and no LDS staging beyond the row reduction.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vqk.h"
+#include "vqk_internal.h"
+#include "vqk_math.h"
+
+namespace vqk {
+
+constexpr int QT = 256;
+
+__device__ __forceinline__ float block_max(float m, float* red) {
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(QT) quant_rows_int8_kernel(const void* w, int dt, int64_t K, int64_t ldw,
+                                                              int8_t* q, void* sout, int s_f32) {
+  __shared__ float red[QT / 64];
+  const int64_t row = blockIdx.x;
+  const int64_t off = row * ldw;
+  float m = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += QT) m = fmaxf(m, fabsf(load_as_f32(w, dt, off + k)));
+  m = block_max(m, red);
+  const float s = fmaxf(m / 127.0f, 1e-12f);
+  for (int64_t k = threadIdx.x; k < K; k += QT) {
+    float v = __builtin_rintf(load_as_f32(w, dt, off + k) / s);
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    q[row * K + k] = (int8_t)(int)v;
+  }
+  if (threadIdx.x == 0) {
+    if (s_f32) ((float*)sout)[row] = s;
+    else ((uint16_t*)sout)[row] = f2h(s);
+  }
+}
+
+__global__ void __launch_bounds__(QT) quant_rows_fp8_kernel(const void* w, int dt, int64_t K, int64_t ldw,
+                                                             uint8_t* q, uint16_t* sout) {
+  __shared__ float red[QT / 64];
+  const int64_t row = blockIdx.x;
+  const int64_t off = row * ldw;
+  float m = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += QT) m = fmaxf(m, fabsf(load_as_f32(w, dt, off + k)));
+  m = block_max(m, red);
+  const float s = fmaxf(m / 448.0f, 1e-12f);
+  for (int64_t k = threadIdx.x; k < K; k += QT) {
+    float v = load_as_f32(w, dt, off + k) / s;
+    v = fminf(fmaxf(v, -448.f), 448.f);
+    q[row * K + k] = f32_to_e4m3(v);
+  }
+  if (threadIdx.x == 0) sout[row] = f2h(s);
+}
+
+// One thread per 32-element group.
+__global__ void quant_mx_kernel(const void* t, int dt, int64_t R, int64_t K, int64_t ldt, uint8_t* q,
+                                uint8_t* scales, int fp4) {
+  const int64_t G = K / 32;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= R * G) return;
+  const int64_t row = gid / G, grp = gid - row * G;
+  const int64_t off = row * ldt + grp * 32;
+  float v[32];
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    v[e] = load_as_f32(t, dt, off + e);
+    amax = fmaxf(amax, fabsf(v[e]));
+  }
+  const int k = mx_exponent(amax, fp4 ? 6.0f : 448.0f);
+  const float sc = exp2i(k);
+  scales[row * G + grp] = (uint8_t)(k + 127);
+  if (!fp4) {
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      float y = fminf(fmaxf(v[e] / sc, -448.f), 448.f);
+      w[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
+    }
+    uint32_t* dst = (uint32_t*)(q + row * K + grp * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = w[i];
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 32; ++e) w[e >> 3] |= f32_to_e2m1(v[e] / sc) << (4 * (e & 7));
+    uint32_t* dst = (uint32_t*)(q + row * (K / 2) + grp * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = w[i];
+  }
+}
+
+// Per-tensor INT8 activation quantization: a single workgroup (the activation is tiny).
+__global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int dt, int64_t ldx, int64_t B,
+                                                               int64_t K, int8_t* xq, float* xs) {
+  __shared__ float red[16];
+  float m = 0.f;
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load_as_f32(x, dt, b * ldx + k)));
+  m = block_max(m, red);
+  const float s = fmaxf(m / 127.0f, 1e-12f);
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
+      float v = __builtin_rintf(load_as_f32(x, dt, b * ldx + k) / s);
+      v = fminf(fmaxf(v, -127.f), 127.f);
+      xq[b * K + k] = (int8_t)(int)v;
+    }
+  if (threadIdx.x == 0) *xs = s;
+}
+
+__global__ void act_cast_e4m3_kernel(const void* x, int dt, int64_t ldx, int64_t B, int64_t K, uint8_t* xq) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * K) return;
+  const int64_t b = i / K, k = i - b * K;
+  xq[i] = f32_to_e4m3(load_as_f32(x, dt, b * ldx + k));
+}
+
+static int dt_ok(int dt) { return dt == VQK_F32 || dt == VQK_F16 || dt == VQK_BF16; }
+
+static int finish() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VQK_OK : (int)e;
+}
+
+}  // namespace vqk
+
+using namespace vqk;
+
+extern "C" int vqk_quant_rows_int8(const void* w, int w_dtype, int64_t M, int64_t K, int64_t ldw, int8_t* q,
+                                   void* scale_out, int scale_is_f32, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!w || !q || !scale_out || !dt_ok(w_dtype) || M < 0 || K < 1 || ldw < K) return VQK_EINVAL;
+  if (M == 0) return VQK_OK;
+  if (M > INT32_MAX) return VQK_EUNSUPPORTED;
+  hipLaunchKernelGGL(quant_rows_int8_kernel, dim3((unsigned)M), dim3(QT), 0, (hipStream_t)stream, w, w_dtype,
+                     K, ldw, q, scale_out, scale_is_f32 ? 1 : 0);
+  return finish();
+}
+
+extern "C" int vqk_quant_rows_fp8(const void* w, int w_dtype, int64_t M, int64_t K, int64_t ldw, uint8_t* q,
+                                  uint16_t* scale_f16, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!w || !q || !scale_f16 || !dt_ok(w_dtype) || M < 0 || K < 1 || ldw < K) return VQK_EINVAL;
+  if (M == 0) return VQK_OK;
+  if (M > INT32_MAX) return VQK_EUNSUPPORTED;
+  hipLaunchKernelGGL(quant_rows_fp8_kernel, dim3((unsigned)M), dim3(QT), 0, (hipStream_t)stream, w, w_dtype, K,
+                     ldw, q, scale_f16);
+  return finish();
+}
+
+static int quant_mx(const void* t, int dt, int64_t R, int64_t K, int64_t ldt, uint8_t* q, uint8_t* s, int fp4,
+                    hipStream_t st) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!t || !q || !s || !dt_ok(dt) || R < 0 || K < 1 || ldt < K) return VQK_EINVAL;
+  if (K % 32 != 0) return VQK_EINVAL;
+  if (R == 0) return VQK_OK;
+  const int64_t n = R * (K / 32);
+  const int th = 256;
+  const int64_t nb = (n + th - 1) / th;
+  if (nb > INT32_MAX) return VQK_EUNSUPPORTED;
+  hipLaunchKernelGGL(quant_mx_kernel, dim3((unsigned)nb), dim3(th), 0, st, t, dt, R, K, ldt, q, s, fp4);
+  return finish();
+}
+
+extern "C" int vqk_quant_mxfp8(const void* t, int t_dtype, int64_t R, int64_t K, int64_t ldt, uint8_t* q,
+                               uint8_t* scales, vqk_stream_t stream) {
+  return quant_mx(t, t_dtype, R, K, ldt, q, scales, 0, (hipStream_t)stream);
+}
+
+extern "C" int vqk_quant_mxfp4(const void* t, int t_dtype, int64_t R, int64_t K, int64_t ldt, uint8_t* packed,
+                               uint8_t* scales, vqk_stream_t stream) {
+  return quant_mx(t, t_dtype, R, K, ldt, packed, scales, 1, (hipStream_t)stream);
+}
+
+extern "C" int vqk_act_quant_int8(const void* x, int x_dtype, int64_t ldx, int64_t B, int64_t K, int8_t* xq,
+                                  float* xs, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!x || !xq || !xs || !dt_ok(x_dtype) || B < 0 || K < 1 || ldx < K) return VQK_EINVAL;
+  hipLaunchKernelGGL(act_quant_int8_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, x_dtype, ldx, B, K, xq,
+                     xs);
+  return finish();
+}
+
+extern "C" int vqk_act_cast_e4m3(const void* x, int x_dtype, int64_t ldx, int64_t B, int64_t K, uint8_t* xq,
+                                 vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!x || !xq || !dt_ok(x_dtype) || B < 0 || K < 1 || ldx < K) return VQK_EINVAL;
+  if (B == 0) return VQK_OK;
+  const int64_t n = B * K;
+  hipLaunchKernelGGL(act_cast_e4m3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     x, x_dtype, ldx, B, K, xq);
+  return finish();
+}

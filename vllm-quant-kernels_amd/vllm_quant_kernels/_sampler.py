@@ -1,0 +1,111 @@
+"""Sampler.sample replacement (VLLM_USE_FUSED_SAMPLER=1).
+
+Behaviour follows the reference hook (src/vllm_quant_kernels/_sampler.py:28-214): only
+``Sampler.sample`` is overridden; anything outside the fused fast path (top-p, allowed-token
+masks, bad words, logits processors, thinking budgets, per-request generators, processed
+logprobs) is handed to the upstream implementation unchanged.  The fast path itself is one
+HIP launch (``fused_gumbel_sample``).
+"""
+from __future__ import annotations
+
+import os
+import sys
+from typing import TYPE_CHECKING
+
+import torch
+
+from ._sampler_kernels import fused_gumbel_sample
+
+if TYPE_CHECKING:  # pragma: no cover
+    from vllm.v1.sample.metadata import SamplingMetadata
+
+_SAMPLING_EPS = 1e-5
+
+
+def _fast_path_ok(sampling_metadata: "SamplingMetadata") -> bool:
+    """True when every feature outside the fused kernel is off
+    (reference src/vllm_quant_kernels/_sampler.py:28-59)."""
+    sm = sampling_metadata
+    if sm.top_p is not None or sm.allowed_token_ids_mask is not None:
+        return False
+    if sm.bad_words_token_ids:
+        return False
+    procs = sm.logitsprocs
+    if procs.argmax_invariant or procs.non_argmax_invariant:
+        return False
+    holder = getattr(sm, "thinking_budget_state_holder", None)
+    if holder is not None and holder.has_tracked_requests():
+        return False
+    if sm.generators:
+        return False
+    return True
+
+
+def _compute_topk_threshold(logits: torch.Tensor, top_k: torch.Tensor, vocab_size: int):
+    """Per-row k-th largest raw logit, or None when top-k is off for every row
+    (reference src/vllm_quant_kernels/_sampler.py:62-93)."""
+    max_k = int(top_k.max().item())
+    if max_k >= vocab_size:
+        return None
+    vals, _ = torch.topk(logits, max_k, dim=-1, sorted=True)
+    col = (top_k.clamp(max=max_k) - 1).clamp(min=0).to(torch.int64).unsqueeze(-1)
+    return vals.gather(dim=-1, index=col).squeeze(-1).contiguous()
+
+
+def _make_seeds(batch_size: int, device: torch.device) -> torch.Tensor:
+    """One int32 seed per row from the default device generator
+    (reference src/vllm_quant_kernels/_sampler.py:96-116)."""
+    return torch.randint(0, 2**31 - 1, (batch_size,), dtype=torch.int32, device=device)
+
+
+def install_fused_sampler() -> None:
+    """Rebind vllm.v1.sample.sampler.Sampler to a FusedSampler subclass
+    (reference src/vllm_quant_kernels/_sampler.py:119-214).  Must run before the model
+    runner imports Sampler (i.e. from the vllm.general_plugins entry point)."""
+    import vllm.v1.sample.sampler as upstream_module
+
+    upstream_sampler = upstream_module.Sampler
+    if getattr(upstream_sampler, "_vqk_fused", False):
+        return  # already installed
+
+    class FusedSampler(upstream_sampler):
+        """Upstream Sampler with temperature + top-k + Gumbel argmax fused into one launch."""
+
+        _vqk_fused = True
+
+        def sample(self, logits, sampling_metadata, logprobs_mode_override=None):
+            sm = sampling_metadata
+            if not _fast_path_ok(sm):
+                return super().sample(logits, sm, logprobs_mode_override)
+            mode = logprobs_mode_override or getattr(self, "logprobs_mode", None)
+            wants_logprobs = sm.max_num_logprobs is not None or bool(getattr(sm, "logprob_token_ids", None))
+            if wants_logprobs and mode in ("processed_logits", "processed_logprobs"):
+                return super().sample(logits, sm, logprobs_mode_override)
+            if sm.all_greedy:
+                return logits.argmax(dim=-1).view(-1), None
+            assert sm.temperature is not None
+            B, V = logits.shape
+            thr = None
+            if sm.top_k is not None:
+                thr = _compute_topk_threshold(logits, sm.top_k, V)
+            seeds = _make_seeds(B, logits.device)
+            sampled = fused_gumbel_sample(
+                logits=logits,
+                temperature=sm.temperature.to(torch.float32),
+                seeds=seeds,
+                topk_threshold=thr,
+            )
+            return sampled, None
+
+    FusedSampler.__name__ = "FusedSampler"
+    FusedSampler.__qualname__ = "FusedSampler"
+    upstream_module.Sampler = FusedSampler
+    print("[vllm-quant-kernels] FusedSampler installed (vllm.v1.sample.sampler.Sampler patched).",
+          file=sys.stderr, flush=True)
+
+
+def env_bool(name: str, default: bool = False) -> bool:
+    val = os.environ.get(name, "")
+    if val == "":
+        return default
+    return val.lower() in ("1", "true", "yes", "on")

@@ -1,0 +1,101 @@
+"""Fused Gumbel-argmax sampling over [B, V] fp32 logits, one HIP launch.
+
+Replaces the reference's Triton block-argmax kernel plus its two-op host tail
+(src/vllm_quant_kernels/_sampler_kernels.py:38-182) with ``vqk_gumbel_argmax``: the
+temperature scaling, Philox noise, top-k masking, per-slice argmax and the cross-slice
+reduction all happen inside one kernel that reads the logits once.
+
+Per row b and vocab index v the kernel takes the argmax (smallest index on ties) of
+  y = x                                  if temperature is None or temperature[b] < 1e-5,
+  y = x / temperature[b] + G(seed_b, v)  otherwise,
+with y = -inf where topk_threshold is given and x < topk_threshold[b] (raw logits).
+G = -log(-log(max(u, 2^-126))) and u is Triton's tl.rand(seed, v) (Philox4x32-10, word 0
+of counter (v,0,0,0), key = the seed widened to 64 bits), so a given (seed, v) draws the
+same uniform as the reference.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_GREEDY_EPS = 1e-5
+_ws_lock = threading.Lock()
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, stream: int, B: int) -> torch.Tensor:
+    """Per (device, stream) zero-initialised workspace; the kernel leaves it zeroed again,
+    so it is cleared only when first created or grown.  Launches on one stream are ordered,
+    so sharing it among them is safe; different streams get different workspaces."""
+    need = int(_lib.load().vqk_gumbel_workspace_size(B))
+    key = (device.index, stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(max(need, 4096), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+    return ws
+
+
+def fused_gumbel_sample(
+    logits: torch.Tensor,                         # [B, V] fp32
+    temperature: torch.Tensor | None,             # [B] fp32 (None => plain argmax)
+    seeds: torch.Tensor,                          # [B] int32 (or int64)
+    topk_threshold: torch.Tensor | None = None,   # [B] fp32 or None
+    block_size: int = 1024,
+) -> torch.Tensor:
+    """Fused Gumbel-argmax sampling; returns [B] int64 token ids.
+
+    Same contract as the reference function (src/vllm_quant_kernels/_sampler_kernels.py:123-182);
+    ``block_size`` is accepted for signature compatibility and does not change the result
+    (the noise depends only on (seed, v)).  int64 seeds are accepted as an extension: the
+    full 64 bits key the Philox stream.
+    """
+    B, V = logits.shape
+    assert logits.dtype == torch.float32, f"Fused sampler requires fp32 logits, got {logits.dtype}"
+    assert logits.is_contiguous(), "Fused sampler requires contiguous logits"
+    assert seeds.shape == (B,) and seeds.dtype in (torch.int32, torch.int64)
+    if temperature is not None:
+        assert temperature.shape == (B,) and temperature.dtype == torch.float32
+    if topk_threshold is not None:
+        assert topk_threshold.shape == (B,) and topk_threshold.dtype == torch.float32
+    if not logits.is_cuda:
+        raise ValueError("fused_gumbel_sample: logits must live on the ROCm device")
+    seeds = seeds.contiguous()
+    temperature = temperature.contiguous() if temperature is not None else None
+    topk_threshold = topk_threshold.contiguous() if topk_threshold is not None else None
+    out = torch.empty(B, dtype=torch.int64, device=logits.device)
+    if B == 0:
+        return out
+    stream = torch.cuda.current_stream(logits.device).cuda_stream
+    ws = _workspace(logits.device, stream, B)
+    _lib.call(
+        "vqk_gumbel_argmax",
+        logits.data_ptr(), logits.stride(0), B, V,
+        temperature.data_ptr() if temperature is not None else None,
+        seeds.data_ptr(), 1 if seeds.dtype == torch.int64 else 0,
+        topk_threshold.data_ptr() if topk_threshold is not None else None,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+    )
+    return out
+
+
+def gumbel_scores(logits, temperature, seeds, topk_threshold=None) -> torch.Tensor:
+    """Debug: the [B, V] fp32 values the sampler takes its argmax over."""
+    B, V = logits.shape
+    assert logits.dtype == torch.float32 and logits.is_contiguous()
+    seeds = seeds.contiguous()
+    scores = torch.empty(B, V, dtype=torch.float32, device=logits.device)
+    stream = torch.cuda.current_stream(logits.device).cuda_stream
+    _lib.call(
+        "vqk_gumbel_scores",
+        logits.data_ptr(), logits.stride(0), B, V,
+        temperature.data_ptr() if temperature is not None else None,
+        seeds.data_ptr(), 1 if seeds.dtype == torch.int64 else 0,
+        topk_threshold.data_ptr() if topk_threshold is not None else None,
+        scores.data_ptr(), stream,
+    )
+    return scores
