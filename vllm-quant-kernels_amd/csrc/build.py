@@ -39,15 +39,15 @@ def flags():
     ]
 
 
-def build(out=DEFAULT_OUT, jobs=4, save_temps=None, verbose=False):
+def build(out=DEFAULT_OUT, jobs=4, save_temps=None, verbose=False, defines=()):
     cc = hipcc()
-    objdir = os.path.join(REPO, "_build", "obj")
+    objdir = os.path.join(REPO, "_build", "obj" + "".join("_" + d.replace("=", "") for d in defines))
     os.makedirs(objdir, exist_ok=True)
     os.makedirs(os.path.dirname(out), exist_ok=True)
 
     def compile_one(src):
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
-        cmd = [cc] + flags() + ["-c", os.path.join(HERE, src), "-o", obj]
+        cmd = [cc] + flags() + [f"-D{d}" for d in defines] + ["-c", os.path.join(HERE, src), "-o", obj]
         if save_temps:
             os.makedirs(save_temps, exist_ok=True)
             cmd += ["-save-temps=obj"]
@@ -77,6 +77,7 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("--save-temps", default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("-D", dest="defines", action="append", default=[], help="extra preprocessor define")
     a = ap.parse_args()
-    print(build(a.out, a.jobs, a.save_temps, a.verbose))
+    print(build(a.out, a.jobs, a.save_temps, a.verbose, tuple(a.defines)))
     sys.exit(0)

@@ -35,6 +35,22 @@
 #include "vqk_internal.h"
 #include "vqk_math.h"
 
+// Build-time tuning knobs (defaults are the measured choice).
+#ifndef VQK_LM_NT
+#define VQK_LM_NT 0        // 1: non-temporal weight loads (measured slower on MI355X)
+#endif
+#ifndef VQK_LM_WG_PER_CU
+#define VQK_LM_WG_PER_CU 2 // persistent workgroups per CU when the LDS footprint allows
+#endif
+#ifndef VQK_LM_DEPTH
+#define VQK_LM_DEPTH 4     // largest register-ring depth (chunks in flight per wave)
+#endif
+#if VQK_LM_NT
+#define VQK_LOAD(p) __builtin_nontemporal_load(p)
+#else
+#define VQK_LOAD(p) (*(p))
+#endif
+
 namespace vqk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -56,22 +72,26 @@ template <> struct ModeTraits<M_FP8>   { enum { MPC = 1, FB = 32, XB = 1, KPM = 
 template <> struct ModeTraits<M_MXFP8> { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
 template <> struct ModeTraits<M_MXFP4> { enum { MPC = 2, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
 
-// k offset (within a row) of the first element of B fragment (mi, g): the k positions a
-// lane of k-block g holds for the mi-th MFMA of a row.  Must match the weight addressing
-// in load_chunk(): chunk c = bytes [128c, 128c+128) of the row.
+// Memory k of the activation element feeding byte/element p of lane k-block g's B fragment
+// for the mi-th MFMA of a row.  It must pair with the weight addressing in load_chunk():
+//  * W8A16 (16x16x32 f16, 8 elements per lane): mi = 4c + 2h + q, lane bytes
+//    [128c + 64h + 16g, +16) of the row, q-th 8-byte half -> k = 128c + 64h + 16g + 8q + p;
+//  * W8A8 (16x16x64 i8, 16 per lane): mi = 2c + h -> k = 128c + 64h + 16g + p;
+//  * FP8 / MXFP8 / MXFP4 activations (16x16x128 f8f6f4, 32 per lane): the matrix core
+//    reads a lane's 32 values as two halves, value p <-> k = 64*(p/16) + 16g + p%16 within
+//    the MFMA's 128-k block, and 32-k scale block j = [32j, 32j+32) takes its E8M0 byte from
+//    k-block lane j.  Mapping the MFMA's 128 k onto row k [128mi, 128mi + 128) in order
+//    makes every scale block one MX group (4mi + j) of the row.
 template <int MODE>
-__device__ __forceinline__ int frag_k0(int mi, int g) {
-  if (MODE == M_W8A16) {  // mi = 4c + 2h + q; lane bytes [128c + 64h + 16g, +16), q-th half
+__device__ __forceinline__ int frag_k(int mi, int g, int p) {
+  if (MODE == M_W8A16) {
     int c = mi >> 2, h = (mi >> 1) & 1, q = mi & 1;
-    return 128 * c + 64 * h + 16 * g + 8 * q;
-  } else if (MODE == M_W8A8) {  // mi = 2c + h; bytes [128c + 64h + 16g, +16)
+    return 128 * c + 64 * h + 16 * g + 8 * q + p;
+  } else if (MODE == M_W8A8) {
     int c = mi >> 1, h = mi & 1;
-    return 128 * c + 64 * h + 16 * g;
-  } else if (MODE == M_MXFP4) {  // mi = 2c + h; bytes [128c + 64h + 16g, +16) = k [256c+128h+32g, +32)
-    int c = mi >> 1, h = mi & 1;
-    return 256 * c + 128 * h + 32 * g;
-  } else {  // FP8 / MXFP8: mi = c; bytes [128c + 32g, +32)
-    return 128 * mi + 32 * g;
+    return 128 * c + 64 * h + 16 * g + p;
+  } else {
+    return 128 * mi + 64 * (p >> 4) + 16 * g + (p & 15);
   }
 }
 
@@ -126,50 +146,22 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
     if (tid == 0) lds_red[16] = xs_w8a8;
   }
 
-  for (int f = tid; f < nfrag; f += nth) {
-    int b = f % Bg;
-    int gm = f / Bg;
-    int g = gm & 3, mi = gm >> 2;
-    int k0 = frag_k0<MODE>(mi, g);
-    uint8_t* dst = lds + (size_t)f * T::FB;
-    const int64_t xo = (int64_t)b * a.ldx + k0;
-    if (MODE == M_W8A16) {
-      const uint16_t* src = (const uint16_t*)a.x + xo;
-      uint32_t v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
-      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-    } else if ((MODE == M_W8A8 || MODE == M_FP8) && a.xq) {
-      // pre-quantized int8 / e4m3 activations [Bg, K]: copy the fragment's bytes
-      const uint8_t* src = a.xq + (int64_t)b * K + k0;
-#pragma unroll
-      for (int e = 0; e < T::FB; e += 4)
-        *(uint32_t*)(dst + e) = (uint32_t)src[e] | ((uint32_t)src[e + 1] << 8) | ((uint32_t)src[e + 2] << 16) |
-                                ((uint32_t)src[e + 3] << 24);
-    } else if (MODE == M_W8A8) {
-      uint32_t v[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float q = __builtin_rintf(load_as_f32(a.x, a.xdt, xo + e) / xs_w8a8);
-        q = fminf(fmaxf(q, -127.f), 127.f);
-        v[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)(int)q) << (8 * (e & 3));
-      }
-      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-    } else if (MODE == M_FP8) {
-      uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)f32_to_e4m3(load_as_f32(a.x, a.xdt, xo + e)) << (8 * (e & 3));
-      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-      *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
-    } else {  // MX: one 32-element group per fragment
+  if constexpr (T::MX) {
+    // one 32-element MX group per work item; its 32 bytes land in two 16-byte halves of the
+    // fragments of lanes g = 2(j%2) and 2(j%2)+1 (j = group % 4), at byte 16*(j/2)
+    const int G = K / 32;
+    for (int f = tid; f < G * Bg; f += nth) {
+      const int b = f % Bg, grp = f / Bg;
+      const int mi = grp >> 2, j = grp & 3;
       uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
       uint32_t sbyte;
       if (a.xq) {
-        const uint8_t* src = a.xq + (int64_t)b * K + k0;
+        const uint8_t* src = a.xq + (int64_t)b * K + 32 * grp;
 #pragma unroll
         for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
-        sbyte = a.xsq[(int64_t)b * (K / 32) + (k0 >> 5)];
+        sbyte = a.xsq[(int64_t)b * G + grp];
       } else {
+        const int64_t xo = (int64_t)b * a.ldx + 32 * grp;
         float xv[32];
         float amax = 0.f;
 #pragma unroll
@@ -186,11 +178,47 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
         }
         sbyte = (uint32_t)(kx + 127);
       }
-      *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-      *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
-      // scale byte: gather per dword below (byte writes into LDS are fine on gfx950)
-      uint8_t* sdst = (uint8_t*)(lds_xs + ((size_t)((mi >> 2) * 4 + g) * Bg + b)) + (mi & 3);
+      const int g0 = 2 * (j & 1), off = 16 * (j >> 1);
+      uint8_t* d0 = lds + (size_t)((mi * 4 + g0) * Bg + b) * T::FB + off;
+      uint8_t* d1 = lds + (size_t)((mi * 4 + g0 + 1) * Bg + b) * T::FB + off;
+      *(uint4*)d0 = make_uint4(v[0], v[1], v[2], v[3]);
+      *(uint4*)d1 = make_uint4(v[4], v[5], v[6], v[7]);
+      uint8_t* sdst = (uint8_t*)(lds_xs + ((size_t)((mi >> 2) * 4 + j) * Bg + b)) + (mi & 3);
       *sdst = (uint8_t)sbyte;
+    }
+  } else {
+    for (int f = tid; f < nfrag; f += nth) {
+      const int b = f % Bg;
+      const int gm = f / Bg;
+      const int g = gm & 3, mi = gm >> 2;
+      uint8_t* dst = lds + (size_t)f * T::FB;
+      if (MODE == M_W8A16) {
+        const uint16_t* src = (const uint16_t*)a.x + (int64_t)b * a.ldx + frag_k<MODE>(mi, g, 0);
+        uint32_t v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+        *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+      } else {
+        // W8A8 (16 bytes) or FP8 (32 bytes): element p of the fragment is row element frag_k(p)
+        uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int p = 0; p < T::FB; ++p) {
+          const int k = frag_k<MODE>(mi, g, p);
+          uint32_t byte;
+          if (a.xq) {
+            byte = a.xq[(int64_t)b * K + k];
+          } else if (MODE == M_W8A8) {
+            float q = __builtin_rintf(load_as_f32(a.x, a.xdt, (int64_t)b * a.ldx + k) / xs_w8a8);
+            q = fminf(fmaxf(q, -127.f), 127.f);
+            byte = (uint32_t)(uint8_t)(int8_t)(int)q;
+          } else {
+            byte = f32_to_e4m3(load_as_f32(a.x, a.xdt, (int64_t)b * a.ldx + k));
+          }
+          v[p >> 2] |= byte << (8 * (p & 3));
+        }
+        *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+        if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
+      }
     }
   }
   if (T::MX) {
@@ -221,21 +249,25 @@ struct Slot<M_MXFP8> {
   uint32_t s0, s1;
 };
 
+// Loads lane k-block g's share of 128-byte chunk c of its row: two 16-byte pieces at
+// [128c + 16g] and [128c + 64 + 16g], plus the chunk's MX scale dwords.  For the 8-bit
+// operands the two pieces are the two halves the matrix core pairs with the activation
+// halves (frag_k); for E2M1 each piece is one MFMA's A operand: 32 consecutive k of the row,
+// i.e. one whole MX group (the fp4 A layout is 32 contiguous k per lane).
 template <int MODE>
 __device__ __forceinline__ void load_chunk(Slot<MODE>& s, const uint8_t* rowp, const uint32_t* srowp,
                                            int c, int g) {
+  v4i lo = VQK_LOAD((const v4i*)(rowp + 128 * c + 16 * g));
+  v4i hi = VQK_LOAD((const v4i*)(rowp + 128 * c + 64 + 16 * g));
   if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
-    const v4i* p = (const v4i*)(rowp + 128 * c + 32 * g);
-    v4i lo = __builtin_nontemporal_load(p);
-    v4i hi = __builtin_nontemporal_load(p + 1);
     s.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   } else {
-    s.lo = __builtin_nontemporal_load((const v4i*)(rowp + 128 * c + 16 * g));
-    s.hi = __builtin_nontemporal_load((const v4i*)(rowp + 128 * c + 64 + 16 * g));
+    s.lo = lo;
+    s.hi = hi;
   }
-  if (MODE == M_MXFP8) {
+  if constexpr (MODE == M_MXFP8) {
     s.s0 = srowp[c];
-  } else if (MODE == M_MXFP4) {
+  } else if constexpr (MODE == M_MXFP4) {
     s.s0 = srowp[2 * c];
     s.s1 = srowp[2 * c + 1];
   }
@@ -480,6 +512,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
 // ---------------------------------------------------------------------------------------
 // Host side
 static int pick_depth(int cpr) {
+  if (VQK_LM_DEPTH >= 8 && cpr % 8 == 0) return 8;
+  if (VQK_LM_DEPTH >= 6 && cpr % 6 == 0) return 6;
   if (cpr % 4 == 0) return 4;
   if (cpr % 2 == 0) return 2;
   return 1;
@@ -494,6 +528,12 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
     hipLaunchKernelGGL((lmhead_kernel<MODE, NCT, DD>), dim3(grid), dim3(threads), lds_bytes, st, a); \
     break;
     VQK_L(1) VQK_L(2) VQK_L(4)
+#if VQK_LM_DEPTH >= 6
+    VQK_L(6)
+#endif
+#if VQK_LM_DEPTH >= 8
+    VQK_L(8)
+#endif
 #undef VQK_L
     default:
       return VQK_EINVAL;
@@ -559,7 +599,9 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     size_t lds = (size_t)NMF * 4 * Bg * T::FB + T::FB;
     if (T::MX) lds += ((size_t)((NMF + 3) / 4) * 4 * Bg + 1) * 4;
     lds = (lds + 15) & ~(size_t)15;
-    const int per_cu = (lds <= 48 * 1024) ? 2 : 1;
+    int per_cu = (int)((150 * 1024) / (lds + 1024));
+    if (per_cu > VQK_LM_WG_PER_CU) per_cu = VQK_LM_WG_PER_CU;
+    if (per_cu < 1) per_cu = 1;
     const int ntiles = (int)((M + 15) / 16);
     int grid = ncu * per_cu;
     const int max_grid = (ntiles + (threads / 64) - 1) / (threads / 64);

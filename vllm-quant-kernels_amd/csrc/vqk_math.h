@@ -20,8 +20,12 @@ __device__ __forceinline__ float h2f(uint16_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, h);
   return (float)v;
 }
-// float -> fp16 bits, round to nearest even (hardware v_cvt_f16_f32).
+// float -> fp16 bits, round to nearest even (hardware v_cvt_f16_f32).  The empty asm
+// pins f as a float32 register value first: otherwise the backend may fold a preceding
+// multiply into v_fma_mix (one rounding straight to fp16), while the reference rounds the
+// product to float32 and then to fp16.
 __device__ __forceinline__ uint16_t f2h(float f) {
+  asm volatile("" : "+v"(f));
   _Float16 v = (_Float16)f;
   return __builtin_bit_cast(uint16_t, v);
 }

@@ -9,13 +9,14 @@
 // G = -log(-log(max(u, 2^-126))) with u = Triton's tl.rand(seed, v): Philox4x32-10 word 0
 // of counter (v, 0, 0, 0) under key (seed lo32, seed hi32).
 //
-// Design (MI355X): one workgroup of 256 threads per 4096-element slice of a row; each
-// thread holds 16 logits from four coalesced 16-byte loads, so the logits are read from
+// Design (MI355X): one workgroup of 256 threads per 8192-element slice of a row; each
+// thread holds 32 logits from eight coalesced 16-byte loads, so the logits are read from
 // HBM exactly once.  The Philox/log work is the expensive part (~150 VALU ops per element),
 // so the kernel prunes exactly instead of computing noise everywhere:
 //   * every thread first scores its own largest raw logit (one Philox each, in parallel);
-//     the best of those, merged with the row's running best published by other slices
-//     through a 64-bit atomicMax, is a value L that the row's winner is >= to;
+//     each slice publishes the best of those with a 64-bit atomicMax and waits (bounded
+//     in time, so it can never deadlock) until all slices of its row have published; the
+//     row's best candidate L is then a value the row's winner is >= to;
 //   * since G <= GUMBEL_MAX for every possible u, an element with
 //     fl(fl(x/T) + GUMBEL_MAX) < L can never win (rounding is monotone), and that test
 //     reduces to one compare of the raw logit against a per-row cutoff;
@@ -35,7 +36,7 @@ namespace vqk {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int SMP_THREADS = 256;
-constexpr int SMP_EPT = 16;                               // elements per thread
+constexpr int SMP_EPT = 32;                               // elements per thread
 constexpr int SMP_CHUNK = SMP_THREADS * SMP_EPT;          // elements per workgroup
 constexpr float GREEDY_EPS = 1e-5f;
 
@@ -48,10 +49,12 @@ struct SmpArgs {
   int seed64;
   const float* thr;
   int64_t* out;
-  unsigned long long* keys;  // [B]
-  unsigned int* counters;    // [B]
+  unsigned long long* keys;  // [B] row best key
+  unsigned int* arrive;      // [B] slices that published their candidates
+  unsigned int* done;        // [B] slices finished
   int nchunks;
   int vec;                   // 16-byte loads allowed
+  uint64_t wait_ticks;       // bound of the wait for the row's other slices (wall clock)
   float* scores;             // debug: write y for every element (scores kernel only)
 };
 
@@ -106,11 +109,35 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
   return k;
 }
 
+// Cross-workgroup protocol.  Only device-scope atomics on the workspace are used, relaxed:
+// acquire/release fences would write back and invalidate the L2 of the issuing XCD
+// (buffer_wbl2 / buffer_inv), which costs far more than the whole reduction.  Ordering that
+// matters is enforced by waiting for an atomic's return (s_waitcnt) before the next one:
+//  * a slice's key max is performed before its arrive/done increment is issued;
+//  * the last slice (the one whose done increment returns nchunks-1) reads the key after
+//    that increment returned, so it sees every slice's max.
+// Any key value read earlier is a real candidate's key, hence always a valid pruning bound.
+__device__ __forceinline__ unsigned long long ld_relaxed_u64(unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned int ld_relaxed_u32(unsigned int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long amax_u64(unsigned long long* p, unsigned long long v) {
+  return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned int aadd_u32(unsigned int* p, unsigned int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+constexpr int QCAP = 128;  // per-wave survivor queue (entries)
+
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
   __shared__ unsigned long long red[SMP_THREADS / 64];
-  __shared__ float cand_x[SMP_THREADS / 64][SMP_EPT * 64];
-  __shared__ uint32_t cand_v[SMP_THREADS / 64][SMP_EPT * 64];
-  __shared__ int last_flag;
+  __shared__ float qx[SMP_THREADS / 64][QCAP];
+  __shared__ uint32_t qv[SMP_THREADS / 64][QCAP];
+  __shared__ unsigned long long row_best;
 
   const int row = blockIdx.y;
   const int chunk = blockIdx.x;
@@ -120,11 +147,11 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
   const RowParams p = row_params(a, row);
   const float NEG_INF = -__builtin_inff();
 
-  // ---- load 16 logits per thread (element e of load i sits at base + (i*256 + tid)*4 + e)
+  // ---- load 32 logits per thread (element e of load i sits at base + (i*256 + tid)*4 + e)
   float x[SMP_EPT];
   if (a.vec && base + SMP_CHUNK <= a.V) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < SMP_EPT / 4; ++i) {
       v4f t = __builtin_nontemporal_load((const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4));
       x[4 * i + 0] = t.x;
       x[4 * i + 1] = t.y;
@@ -133,7 +160,7 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < SMP_EPT / 4; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         int v = base + (i * SMP_THREADS + tid) * 4 + e;
@@ -142,93 +169,111 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
   }
   auto vidx = [&](int q) -> uint32_t { return (uint32_t)(base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3)); };
   auto valid = [&](int q) -> bool { return (int)vidx(q) < a.V; };
+  auto admissible = [&](int q) -> bool { return !(p.has_thr && !(x[q] >= p.thr)); };
 
   unsigned long long best = 0ull;  // below every real key
   if (p.greedy) {
 #pragma unroll
     for (int q = 0; q < SMP_EPT; ++q) {
       if (!valid(q)) continue;
-      float y = (p.has_thr && !(x[q] >= p.thr)) ? NEG_INF : x[q];
+      float y = admissible(q) ? x[q] : NEG_INF;
       unsigned long long k = make_key(y, vidx(q));
       best = (k > best) ? k : best;
     }
   } else {
-    // 1) each thread scores its largest admissible raw logit (ties -> smallest index)
+    // 1) each thread scores its largest admissible raw logit (ties -> smallest index);
+    //    inadmissible elements still compete as -inf, as in the reference's masking
     int qm = -1;
     float xm = NEG_INF;
 #pragma unroll
     for (int q = 0; q < SMP_EPT; ++q) {
-      bool ok = valid(q) && !(p.has_thr && !(x[q] >= p.thr));
-      if (ok && (qm < 0 || x[q] > xm)) {
+      if (!valid(q)) continue;
+      if (!admissible(q)) {
+        unsigned long long k = make_key(NEG_INF, vidx(q));
+        best = (k > best) ? k : best;
+      } else if (qm < 0 || x[q] > xm) {
         qm = q;
         xm = x[q];
       }
     }
-    if (qm >= 0) best = make_key(score(p, xm, vidx(qm)), vidx(qm));
-    // elements that are not admissible still compete as -inf (they can only win when
-    // nothing else in the row is admissible, as in the reference's -inf masking)
-#pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
-      if (valid(q) && q != qm && p.has_thr && !(x[q] >= p.thr)) {
-        unsigned long long k = make_key(NEG_INF, vidx(q));
-        best = (k > best) ? k : best;
-      }
+    if (qm >= 0) {
+      unsigned long long k = make_key(score(p, xm, vidx(qm)), vidx(qm));
+      best = (k > best) ? k : best;
     }
-    // 2) workgroup best -> publish to the row, fetch what other slices published
+    // 2) publish this slice's best to the row; wait (bounded) until every slice of the
+    //    row has published, so the pruning bound below is the row-wide one.  The wait
+    //    only affects speed: the pruning is exact with whatever bound is visible.
     unsigned long long wb = wave_max_u64(best);
     if (lane == 0) red[wave] = wb;
     __syncthreads();
-    unsigned long long gb = red[0];
+    if (tid == 0) {
+      unsigned long long gb = red[0];
 #pragma unroll
-    for (int w = 1; w < SMP_THREADS / 64; ++w) gb = (red[w] > gb) ? red[w] : gb;
+      for (int w = 1; w < SMP_THREADS / 64; ++w) gb = (red[w] > gb) ? red[w] : gb;
+      amax_u64(&a.keys[row], gb);
+      wait_vmem();
+      aadd_u32(&a.arrive[row], 1u);
+      const uint64_t t0 = wall_clock64();
+      while (ld_relaxed_u32(&a.arrive[row]) < (unsigned int)a.nchunks && wall_clock64() - t0 < a.wait_ticks)
+        __builtin_amdgcn_s_sleep(8);
+      row_best = ld_relaxed_u64(&a.keys[row]);
+    }
     __syncthreads();
-    // (all threads read the same gb; one atomic publishes it and returns the row's best)
-    __shared__ unsigned long long row_prev;
-    if (tid == 0) row_prev = atomicMax(&a.keys[row], gb);
-    __syncthreads();
-    unsigned long long lk = (row_prev > gb) ? row_prev : gb;
-    float L = from_orderable((uint32_t)(lk >> 32));
-    // 3) raw-logit cutoff xc with fl(fl(xc/T) + GUMBEL_MAX) < L; prune x <= xc
+    const unsigned long long lk = row_best;
+    const float L = from_orderable((uint32_t)(lk >> 32));
+    // 3) raw-logit cutoff xc with fl(fl(xc/T) + GUMBEL_MAX) < L; elements with x <= xc
+    //    cannot reach L (G <= GUMBEL_MAX for every Philox word; rounding is monotone)
     float xc = NEG_INF;
-    if (lk != 0ull && L > NEG_INF && L == L) {
+    if (L > NEG_INF && L == L) {
       float c = (L - GUMBEL_MAX) * p.T;
       for (int it = 0; it < 16; ++it) {
         if ((c / p.T) + GUMBEL_MAX < L) {
           xc = c;
           break;
         }
-        float step = fmaxf(fabsf(c) * 1.1920929e-7f * 4.0f, 1e-30f);
-        c = c - step;
+        c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
       }
     }
-    // 4) compact survivors (x > xc, admissible, not already scored) per wave into LDS
-    int nsurv = 0;
+    // 4) score the survivors through a per-wave queue: full 64-lane batches of Philox work
+    //    instead of mostly-masked lanes
+    int qn = 0;
 #pragma unroll
     for (int q = 0; q < SMP_EPT; ++q) {
-      bool s = valid(q) && q != qm && !(x[q] <= xc) && !(p.has_thr && !(x[q] >= p.thr));
-      unsigned long long m = __ballot(s);
-      if (m) {
-        int pos = nsurv + __popcll(m & ((1ull << lane) - 1ull));
-        if (s) {
-          cand_x[wave][pos] = x[q];
-          cand_v[wave][pos] = vidx(q);
+      const bool s = valid(q) && q != qm && admissible(q) && !(x[q] <= xc);
+      const unsigned long long m = __ballot(s);
+      if (m == 0ull) continue;
+      const int pos = qn + __popcll(m & ((1ull << lane) - 1ull));
+      if (s) {
+        qx[wave][pos] = x[q];
+        qv[wave][pos] = vidx(q);
+      }
+      qn += __popcll(m);
+      __builtin_amdgcn_wave_barrier();
+      if (qn >= 64) {
+        const float xv = qx[wave][lane];
+        const uint32_t v = qv[wave][lane];
+        const float xr = (qn - 64 > lane) ? qx[wave][64 + lane] : 0.f;
+        const uint32_t vr = (qn - 64 > lane) ? qv[wave][64 + lane] : 0u;
+        __builtin_amdgcn_wave_barrier();
+        if (qn - 64 > lane) {
+          qx[wave][lane] = xr;
+          qv[wave][lane] = vr;
         }
-        nsurv += __popcll(m);
+        qn -= 64;
+        const unsigned long long k = make_key(score(p, xv, v), v);
+        best = (k > best) ? k : best;
+        __builtin_amdgcn_wave_barrier();
       }
     }
-    // wave-private LDS region: no workgroup barrier needed, only the wave's own ordering
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int i = lane; i < nsurv; i += 64) {
-      float xv = cand_x[wave][i];
-      uint32_t v = cand_v[wave][i];
-      unsigned long long k = make_key(score(p, xv, v), v);
+    if (lane < qn) {
+      const float xv = qx[wave][lane];
+      const uint32_t v = qv[wave][lane];
+      const unsigned long long k = make_key(score(p, xv, v), v);
       best = (k > best) ? k : best;
     }
   }
 
-  // ---- workgroup reduce, merge into the row, last slice writes the token
+  // ---- workgroup reduce, merge into the row, last slice writes the token and resets
   unsigned long long wb = wave_max_u64(best);
   if (lane == 0) red[wave] = wb;
   __syncthreads();
@@ -236,18 +281,17 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
     unsigned long long gb = red[0];
 #pragma unroll
     for (int w = 1; w < SMP_THREADS / 64; ++w) gb = (red[w] > gb) ? red[w] : gb;
-    atomicMax(&a.keys[row], gb);
-    __threadfence();
-    unsigned int done = atomicAdd(&a.counters[row], 1u);
-    last_flag = (done == (unsigned int)(a.nchunks - 1));
-  }
-  __syncthreads();
-  if (last_flag && tid == 0) {
-    __threadfence();
-    unsigned long long k = atomicMax(&a.keys[row], 0ull);  // atomic read
-    a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
-    atomicExch(&a.keys[row], 0ull);
-    atomicExch(&a.counters[row], 0u);
+    amax_u64(&a.keys[row], gb);
+    wait_vmem();
+    unsigned int d = aadd_u32(&a.done[row], 1u);
+    if (d == (unsigned int)(a.nchunks - 1)) {
+      // every other slice's max was performed before its done increment
+      unsigned long long k = amax_u64(&a.keys[row], 0ull);
+      a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
+      __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&a.done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -266,7 +310,23 @@ using namespace vqk;
 
 extern "C" int64_t vqk_gumbel_workspace_size(int64_t B) {
   if (B < 0) return 0;
-  return B * (int64_t)(sizeof(unsigned long long) + sizeof(unsigned int)) + 16;
+  return B * (int64_t)(sizeof(unsigned long long) + 2 * sizeof(unsigned int)) + 16;
+}
+
+// Wall-clock ticks per microsecond of the current device (the counter wall_clock64 reads).
+static uint64_t ticks_per_us() {
+  static thread_local int dev_cached = -1;
+  static thread_local uint64_t tpu = 100;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return tpu;
+  if (dev != dev_cached) {
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
+      tpu = (uint64_t)khz / 1000u;
+    if (tpu == 0) tpu = 1;
+    dev_cached = dev;
+  }
+  return tpu;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
@@ -298,7 +358,9 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.thr = topk_thr;
   a.out = out;
   a.keys = (unsigned long long*)workspace;
-  a.counters = (unsigned int*)((char*)workspace + B * sizeof(unsigned long long));
+  a.arrive = (unsigned int*)((char*)workspace + B * sizeof(unsigned long long));
+  a.done = a.arrive + B;
+  a.wait_ticks = 8 * ticks_per_us();
   a.nchunks = (int)((V + SMP_CHUNK - 1) / SMP_CHUNK);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gumbel_argmax_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
