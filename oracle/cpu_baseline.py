@@ -1,9 +1,9 @@
 """TEST INFRASTRUCTURE / BASELINE ONLY - the reference's CPU dequantize-then-matmul.
 
 The reference's lm_head math (src/vllm_quant_kernels/_kernels.py:49-84, with the same
-quantized weights) restated as plain torch CPU fp32 ops, the way BASELINE.md's CPU plan
-describes it: each call dequantizes the int8 weight in 16384-row chunks and runs
-F.linear in fp32.  bench.py times it as the CPU baseline; nothing in the product uses it.
+quantized weights) restated as plain torch CPU fp32 ops: each call dequantizes the int8
+weight in 16384-row chunks and runs F.linear in fp32 (the dequantize-then-matmul of
+tests/test_mxfp4_kernel.py:57-77).  bench.py times it as the CPU baseline; nothing in the product uses it.
 """
 from __future__ import annotations
 

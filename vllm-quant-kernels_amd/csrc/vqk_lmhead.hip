@@ -45,6 +45,18 @@
 #ifndef VQK_LM_DEPTH
 #define VQK_LM_DEPTH 4     // largest register-ring depth (chunks in flight per wave)
 #endif
+#ifndef VQK_LM_LDS
+#define VQK_LM_LDS 1       // stage weights through LDS with direct-to-LDS loads when K allows
+#endif
+#ifndef VQK_LM_LDS_STAGES
+#define VQK_LM_LDS_STAGES 2  // LDS ring depth per wave (4 KB stages)
+#endif
+#ifndef VQK_LM_LDS_WG_PER_CU
+#define VQK_LM_LDS_WG_PER_CU 1
+#endif
+#ifndef VQK_LM_NT_LDS
+#define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
+#endif
 #if VQK_LM_NT
 #define VQK_LOAD(p) __builtin_nontemporal_load(p)
 #else
@@ -65,12 +77,12 @@ template <int MODE>
 struct ModeTraits;
 // MPC: MFMAs per 128-byte chunk of a row; FB: bytes of one lane's B fragment;
 // XB: LDS bytes per activation element; KPM: k values per MFMA (per row);
-// MX: has E8M0 group scales; ACC_INT: int32 accumulator.
-template <> struct ModeTraits<M_W8A16> { enum { MPC = 4, FB = 16, XB = 2, KPM = 32, MX = 0, ACC_INT = 0 }; };
-template <> struct ModeTraits<M_W8A8>  { enum { MPC = 2, FB = 16, XB = 1, KPM = 64, MX = 0, ACC_INT = 1 }; };
-template <> struct ModeTraits<M_FP8>   { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 0, ACC_INT = 0 }; };
-template <> struct ModeTraits<M_MXFP8> { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
-template <> struct ModeTraits<M_MXFP4> { enum { MPC = 2, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0 }; };
+// MX: has E8M0 group scales; ACC_INT: int32 accumulator; ROWSCALE: per-row output scale.
+template <> struct ModeTraits<M_W8A16> { enum { MPC = 4, FB = 16, XB = 2, KPM = 32, MX = 0, ACC_INT = 0, ROWSCALE = 1 }; };
+template <> struct ModeTraits<M_W8A8>  { enum { MPC = 2, FB = 16, XB = 1, KPM = 64, MX = 0, ACC_INT = 1, ROWSCALE = 1 }; };
+template <> struct ModeTraits<M_FP8>   { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 0, ACC_INT = 0, ROWSCALE = 1 }; };
+template <> struct ModeTraits<M_MXFP8> { enum { MPC = 1, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0, ROWSCALE = 0 }; };
+template <> struct ModeTraits<M_MXFP4> { enum { MPC = 2, FB = 32, XB = 1, KPM = 128, MX = 1, ACC_INT = 0, ROWSCALE = 0 }; };
 
 // Memory k of the activation element feeding byte/element p of lane k-block g's B fragment
 // for the mi-th MFMA of a row.  It must pair with the weight addressing in load_chunk():
@@ -110,14 +122,15 @@ struct LmArgs {
   int M, K, Bg, Ball;
   int out_vec;          // 1 when 8-byte output stores are aligned
   float xs_val;         // W8A8 with pre-quantized activations: the per-tensor scale
+  int lds_x_bytes;      // LDS-staged variant: bytes of the activation fragments (16-aligned)
 };
 
 // ---------------------------------------------------------------------------------------
 // Prologue: stage the activations of this batch group into LDS in fragment order.
 // Fragment (mi, g, b) lives at byte ((mi*4 + g) * Bg + b) * FB; a zero fragment follows.
 // MX scales: dword ((mi/4)*4 + g) * Bg + b holds byte (mi % 4) for fragment mi.
-template <int MODE>
-__device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
+template <int MODE, int DT>
+__device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
   typedef ModeTraits<MODE> T;
   const int tid = threadIdx.x, nth = blockDim.x;
   const int K = a.K, Bg = a.Bg;
@@ -130,8 +143,10 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
   if (MODE == M_W8A8 && !a.xq) {
     // per-tensor amax over the whole [Ball, K] activation (bit-exact max, order-free)
     float m = 0.f;
-    for (int b = 0; b < a.Ball; ++b)
-      for (int k = tid; k < K; k += nth) m = fmaxf(m, fabsf(load_as_f32(a.xall, a.xdt, (int64_t)b * a.ldx + k)));
+    for (int b = 0; b < a.Ball; ++b) {
+#pragma unroll 8
+      for (int k = tid; k < K; k += nth) m = fmaxf(m, fabsf(load_dt<DT>(a.xall, (int64_t)b * a.ldx + k)));
+    }
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((tid & 63) == 0) lds_red[tid >> 6] = m;
     __syncthreads();
@@ -166,7 +181,7 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
         float amax = 0.f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
-          xv[e] = load_as_f32(a.x, a.xdt, xo + e);
+          xv[e] = load_dt<DT>(a.x, xo + e);
           amax = fmaxf(amax, fabsf(xv[e]));
         }
         int kx = mx_exponent(amax, 448.0f);
@@ -200,21 +215,28 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
         *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
       } else {
         // W8A8 (16 bytes) or FP8 (32 bytes): element p of the fragment is row element frag_k(p)
+        // (the source test sits outside the element loops so their loads issue together)
         uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if (a.xq) {
 #pragma unroll
-        for (int p = 0; p < T::FB; ++p) {
-          const int k = frag_k<MODE>(mi, g, p);
-          uint32_t byte;
-          if (a.xq) {
-            byte = a.xq[(int64_t)b * K + k];
-          } else if (MODE == M_W8A8) {
-            float q = __builtin_rintf(load_as_f32(a.x, a.xdt, (int64_t)b * a.ldx + k) / xs_w8a8);
-            q = fminf(fmaxf(q, -127.f), 127.f);
-            byte = (uint32_t)(uint8_t)(int8_t)(int)q;
-          } else {
-            byte = f32_to_e4m3(load_as_f32(a.x, a.xdt, (int64_t)b * a.ldx + k));
+          for (int p = 0; p < T::FB; ++p)
+            v[p >> 2] |= (uint32_t)a.xq[(int64_t)b * K + frag_k<MODE>(mi, g, p)] << (8 * (p & 3));
+        } else {
+          float xv[T::FB];
+#pragma unroll
+          for (int p = 0; p < T::FB; ++p) xv[p] = load_dt<DT>(a.x, (int64_t)b * a.ldx + frag_k<MODE>(mi, g, p));
+#pragma unroll
+          for (int p = 0; p < T::FB; ++p) {
+            uint32_t byte;
+            if (MODE == M_W8A8) {
+              float q = __builtin_rintf(xv[p] / xs_w8a8);
+              q = fminf(fmaxf(q, -127.f), 127.f);
+              byte = (uint32_t)(uint8_t)(int8_t)(int)q;
+            } else {
+              byte = f32_to_e4m3(xv[p]);
+            }
+            v[p >> 2] |= byte << (8 * (p & 3));
           }
-          v[p >> 2] |= byte << (8 * (p & 3));
         }
         *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
         if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
@@ -227,6 +249,14 @@ __device__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* 
     if (tid == 0) lds_xs[nsd] = 0x7F7F7F7Fu;
   }
   __syncthreads();
+}
+
+// Activation prologue, dispatched on the activation dtype (pre-quantized input ignores it).
+template <int MODE>
+__device__ __forceinline__ void stage_x(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
+  if (MODE == M_W8A16 || a.xq || a.xdt == VQK_F16) stage_x_dt<MODE, VQK_F16>(a, lds, lds_xs, lds_red);
+  else if (a.xdt == VQK_F32) stage_x_dt<MODE, VQK_F32>(a, lds, lds_xs, lds_red);
+  else stage_x_dt<MODE, VQK_BF16>(a, lds, lds_xs, lds_red);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -380,21 +410,44 @@ __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MO
 
 // Epilogue of one 16-row tile: lane l holds D[4*(l/16) + e][l % 16], e = 0..3, i.e. rows
 // m0 + 4*(l/16) + e of column b = ct*16 + (l % 16).
+// Per-row dequantization scales of the 4 rows m0 + 4*(lane/16) + e a lane's accumulators
+// hold (0 past M).  The loads are clamped to row M-1 rather than predicated, and the raw bits
+// are kept apart from their conversion, so the loads can be issued a whole tile early.
+template <int MODE>
+__device__ __forceinline__ void row_scale_bits(const LmArgs& a, int m0, int lane, uint32_t (&raw)[4]) {
+  const int mr = m0 + 4 * (lane >> 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = (mr + e < a.M) ? (mr + e) : (a.M - 1);
+    if (MODE == M_W8A16 || MODE == M_FP8) raw[e] = ((const uint16_t*)a.ws)[m];
+    else if (MODE == M_W8A8) raw[e] = ((const uint32_t*)a.ws)[m];
+    else raw[e] = 0u;
+  }
+}
+template <int MODE>
+__device__ __forceinline__ void row_scales_from_bits(const LmArgs& a, int m0, int lane, const uint32_t (&raw)[4],
+                                                     float (&sc)[4]) {
+  const int mr = m0 + 4 * (lane >> 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float v = 1.f;
+    if (MODE == M_W8A16 || MODE == M_FP8) v = h2f((uint16_t)raw[e]);
+    else if (MODE == M_W8A8) v = __uint_as_float(raw[e]);
+    sc[e] = (mr + e < a.M) ? v : 0.f;
+  }
+}
+template <int MODE>
+__device__ __forceinline__ void row_scales(const LmArgs& a, int m0, int lane, float (&sc)[4]) {
+  uint32_t raw[4];
+  row_scale_bits<MODE>(a, m0, lane, raw);
+  row_scales_from_bits<MODE>(a, m0, lane, raw, sc);
+}
+
 template <int MODE, int NCT>
 __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, int m0, int lane,
-                                         float xs_w8a8) {
+                                         float xs_w8a8, const float (&sc)[4]) {
   const int g = lane >> 4, j = lane & 15;
   const int mr = m0 + 4 * g;
-  float sc[4] = {1.f, 1.f, 1.f, 1.f};
-  if (MODE == M_W8A16 || MODE == M_FP8) {
-    const uint16_t* s = (const uint16_t*)a.ws;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sc[e] = (mr + e < a.M) ? h2f(s[mr + e]) : 0.f;
-  } else if (MODE == M_W8A8) {
-    const float* s = (const float*)a.ws;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sc[e] = (mr + e < a.M) ? s[mr + e] : 0.f;
-  }
   const bool full = (mr + 3 < a.M);
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
@@ -505,8 +558,209 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
       // raises register pressure (and occupancy is what hides the HBM latency here)
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (c0 + D == CPR) epilogue<MODE, NCT>(acc, a, (wid + tq * total) * 16, lane, xs_w8a8);
+    if (c0 + D == CPR) {
+      float sc[4];
+      row_scales<MODE>(a, (wid + tq * total) * 16, lane, sc);
+      epilogue<MODE, NCT>(acc, a, (wid + tq * total) * 16, lane, xs_w8a8, sc);
+    }
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// LDS-staged variant (the default when K allows it).  Register loads in the MFMA layout touch
+// 16 rows x 64 B per instruction; a plain stream of the weight measured ~6.0 TB/s that way,
+// against ~6.6 TB/s for contiguous non-temporal loads.  So each wave streams its 16-row tile
+// through LDS instead: a stage is 256 B of each of the 16 rows (4 KB), fetched with four
+// global_load_lds_dwordx4 (instruction i: rows 4i..4i+3, 256 contiguous bytes each, 16 lanes
+// per row, non-temporal) straight into the wave's LDS slot, and the MFMA operands are then
+// read with ds_read_b128 in exactly the register layout load_chunk() produces.  Row r's byte c
+// sits at slot + (r/4)*1024 + (r%4)*256 + ((c + 16r) & 255): the rotation by 16r makes the
+// 16 rows of one ds_read_b128 hit distinct bank groups.  S slots per wave form the ring.
+#define VQK_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
+#define VQK_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+constexpr int LDS_STAGE = 4096;
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Row scales of a tile that lies inside M, through the scalar cache: one wave-uniform 32-byte
+// (fp16 scales) or 64-byte (fp32) read per tile.  Scalar loads are counted by lgkmcnt, so the
+// read neither waits for nor delays the weight stream's vmcnt accounting.  Needs a 4-byte
+// aligned scale vector (host-checked).
+template <int MODE>
+__device__ __forceinline__ void tile_scales_smem(const LmArgs& a, int tile, uint32_t (&sdw)[16]) {
+  typedef const __attribute__((address_space(4))) uint32_t* cp32;
+  constexpr int ND = (MODE == M_W8A8) ? 16 : 8;
+  const cp32 sp = (cp32)((uintptr_t)a.ws + (uintptr_t)tile * (4 * ND));
+#pragma unroll
+  for (int i = 0; i < ND; ++i) sdw[i] = sp[i];
+}
+// The 4 raw scales of rows 4g..4g+3 of the tile, out of its uniform dwords.  The dwords
+// pass through readfirstlane so that the selects below stay register selects (a select
+// between array elements would otherwise be folded into an indexed stack load).
+__device__ __forceinline__ uint32_t pick4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, int g) {
+  const uint32_t x01 = (g & 1) ? a1 : a0;
+  const uint32_t x23 = (g & 1) ? a3 : a2;
+  return (g & 2) ? x23 : x01;
+}
+template <int MODE>
+__device__ __forceinline__ void select_tile_scales(const uint32_t (&sdw)[16], int g, uint32_t (&raw)[4]) {
+  constexpr int ND = (MODE == M_W8A8) ? 16 : 8;
+  uint32_t d[16];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) d[i] = __builtin_amdgcn_readfirstlane(sdw[i]);
+  if constexpr (MODE == M_W8A8) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) raw[e] = pick4(d[e], d[4 + e], d[8 + e], d[12 + e], g);
+  } else {
+    const uint32_t lo = pick4(d[0], d[2], d[4], d[6], g);
+    const uint32_t hi = pick4(d[1], d[3], d[5], d[7], g);
+    raw[0] = lo & 0xFFFFu;
+    raw[1] = lo >> 16;
+    raw[2] = hi & 0xFFFFu;
+    raw[3] = hi >> 16;
+  }
+}
+
+template <int MODE>
+struct StageScales {  // MX scale dwords of one stage (2 chunks): MXFP8 2, MXFP4 4
+  uint32_t d[4];
+};
+
+template <int MODE>
+__device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int tile, int ks, uint8_t* slot, int lane,
+                                            StageScales<MODE>& sc) {
+  typedef ModeTraits<MODE> T;
+  const int rr = lane >> 4;            // row within the instruction's 4
+  const int pp = 16 * (lane & 15);     // byte position within the row's 256 in LDS
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * i + rr;
+    int m = tile * 16 + row;
+    m = (m < a.M) ? m : (a.M - 1);
+    const int c = (pp - 16 * row) & 255;  // global byte of the row stored at position pp
+    const uint8_t* src = a.w + (int64_t)m * KB + 256 * ks + c;
+    __builtin_amdgcn_global_load_lds(VQK_GPTR(src), VQK_LPTR(slot + 1024 * i), 16, 0, VQK_LM_NT_LDS);
+  }
+  if constexpr (T::MX) {
+    int m = tile * 16 + (lane & 15);
+    m = (m < a.M) ? m : (a.M - 1);
+    const uint32_t* srow = (const uint32_t*)((const uint8_t*)a.ws + (int64_t)m * (a.K >> 5));
+    if constexpr (MODE == M_MXFP8) {
+      typedef int v2i __attribute__((ext_vector_type(2)));
+      v2i t = *(const v2i*)(srow + 2 * ks);
+      sc.d[0] = (uint32_t)t.x;
+      sc.d[1] = (uint32_t)t.y;
+    } else {
+      v4i t = *(const v4i*)(srow + 4 * ks);
+      sc.d[0] = (uint32_t)t.x;
+      sc.d[1] = (uint32_t)t.y;
+      sc.d[2] = (uint32_t)t.z;
+      sc.d[3] = (uint32_t)t.w;
+    }
+  }
+}
+
+template <int MODE, int NCT, int S>
+__global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
+  typedef ModeTraits<MODE> T;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ float red[17];
+  constexpr int NV = 4 + (T::MX ? 1 : 0);  // vector-memory ops per stage
+  const int K = a.K;
+  const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;
+  const int NMF = K / T::KPM;
+  const int Bg = a.Bg;
+  const uint32_t frag_bytes = (uint32_t)NMF * 4 * Bg * T::FB;
+  uint8_t* lds = smem;
+  uint32_t* lds_xs = (uint32_t*)(smem + frag_bytes + T::FB);
+  const uint32_t zero_off = frag_bytes;
+  const uint32_t xs_pad_idx = (uint32_t)((NMF + 3) / 4) * 4 * Bg;
+  const uint32_t x_bytes = (uint32_t)a.lds_x_bytes;
+
+  stage_x<MODE>(a, lds, lds_xs, red);
+  const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int ntiles = (a.M + 15) >> 4;
+  const int wid = blockIdx.x * nwaves + wave;
+  const int total = gridDim.x * nwaves;
+  if (wid >= ntiles) return;
+  const int my_tiles = (ntiles - 1 - wid) / total + 1;
+  const int SPT = KB >> 8;  // stages per tile (KB % 256 == 0, host guarantees)
+  const int nst = my_tiles * SPT;
+  uint8_t* ring = smem + x_bytes + (uint32_t)wave * S * LDS_STAGE;
+
+  StageScales<MODE> sc[S];
+#pragma unroll
+  for (int s0 = 0; s0 < S; ++s0) {
+    const int q = s0 < nst ? s0 : 0;
+    issue_stage<MODE>(a, KB, wid + (q / SPT) * total, q % SPT, ring + s0 * LDS_STAGE, lane, sc[s0]);
+  }
+  Acc<MODE, NCT> acc;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
+  // lane (r, g) reads row r: base of the row in a slot and its rotation
+  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
+  const int rot = 16 * r;
+  uint32_t sdw[16];  // the tile's row-scale dwords (wave-uniform), fetched at its first stage
+
+  for (int q0 = 0; q0 < nst; q0 += S) {
+#pragma unroll
+    for (int s0 = 0; s0 < S; ++s0) {
+      const int q = q0 + s0;
+      if (q < nst) {
+        wait_vmcnt<(S - 1) * NV>();
+        const uint8_t* slot = ring + s0 * LDS_STAGE + rbase;
+        const int tq = q / SPT, ks = q - tq * SPT;
+        const int tile = wid + tq * total;
+        const bool tile_full = tile * 16 + 16 <= a.M;
+        if (T::ROWSCALE && ks == 0 && tile_full) tile_scales_smem<MODE>(a, tile, sdw);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          Slot<MODE> st;
+          const v4i lo = *(const v4i*)(slot + ((128 * cc + 16 * g + rot) & 255));
+          const v4i hi = *(const v4i*)(slot + ((128 * cc + 64 + 16 * g + rot) & 255));
+          if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
+            st.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          } else {
+            st.lo = lo;
+            st.hi = hi;
+          }
+          if constexpr (MODE == M_MXFP8) {
+            st.s0 = sc[s0].d[cc];
+          } else if constexpr (MODE == M_MXFP4) {
+            st.s0 = sc[s0].d[2 * cc];
+            st.s1 = sc[s0].d[2 * cc + 1];
+          }
+          compute_chunk<MODE, NCT>(acc, st, 2 * ks + cc, g, r, Bg, lds, zero_off, lds_xs, xs_pad_idx);
+        }
+        if (ks == SPT - 1) {
+          float tsc[4];
+          if (!T::ROWSCALE) {
+            tsc[0] = tsc[1] = tsc[2] = tsc[3] = 1.f;
+          } else if (tile_full) {
+            uint32_t raw[4];
+            select_tile_scales<MODE>(sdw, g, raw);
+            row_scales_from_bits<MODE>(a, tile * 16, lane, raw, tsc);
+          } else {
+            row_scales<MODE>(a, tile * 16, lane, tsc);  // the ragged last tile
+          }
+          epilogue<MODE, NCT>(acc, a, tile * 16, lane, xs_w8a8, tsc);
+        }
+        // the slot's ds_reads have completed before the DMA refill may overwrite it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // refill this slot with stage q + S (the DMA waits for this slot's reads: lgkmcnt)
+        const int qn = q + S < nst ? q + S : q;
+        issue_stage<MODE>(a, KB, wid + (qn / SPT) * total, qn % SPT, ring + s0 * LDS_STAGE, lane, sc[s0]);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
 }
 
 // ---------------------------------------------------------------------------------------
@@ -538,6 +792,14 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
     default:
       return VQK_EINVAL;
   }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VQK_OK : (int)e;
+}
+
+template <int MODE, int NCT>
+static int launch_lds(const LmArgs& a, size_t lds_bytes, int grid, hipStream_t st) {
+  // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
+  hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, VQK_LM_LDS_STAGES>), dim3(grid), dim3(256), lds_bytes, st, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }
@@ -599,6 +861,26 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     size_t lds = (size_t)NMF * 4 * Bg * T::FB + T::FB;
     if (T::MX) lds += ((size_t)((NMF + 3) / 4) * 4 * Bg + 1) * 4;
     lds = (lds + 15) & ~(size_t)15;
+    a.lds_x_bytes = (int)lds;
+    const int ntiles_l = (int)((M + 15) / 16);
+    const size_t lds_l = lds + (size_t)4 * VQK_LM_LDS_STAGES * LDS_STAGE;
+    if (VQK_LM_LDS && KB % 256 == 0 && lds_l <= 150 * 1024 && ((uintptr_t)ws & 15) == 0) {
+      int per_cu_l = (int)((150 * 1024) / (lds_l + 512));
+      if (per_cu_l > VQK_LM_LDS_WG_PER_CU) per_cu_l = VQK_LM_LDS_WG_PER_CU;
+      if (per_cu_l < 1) per_cu_l = 1;
+      int grid_l = ncu * per_cu_l;
+      const int max_grid_l = (ntiles_l + 3) / 4;
+      if (grid_l > max_grid_l) grid_l = max_grid_l;
+      const int nct_l = (Bg + 15) / 16;
+      int rcl;
+      if constexpr (MODE == M_W8A16) {
+        rcl = launch_lds<MODE, 1>(a, lds_l, grid_l, st);
+      } else {
+        rcl = (nct_l == 1) ? launch_lds<MODE, 1>(a, lds_l, grid_l, st) : launch_lds<MODE, 2>(a, lds_l, grid_l, st);
+      }
+      if (rcl) return rcl;
+      continue;
+    }
     int per_cu = (int)((150 * 1024) / (lds + 1024));
     if (per_cu > VQK_LM_WG_PER_CU) per_cu = VQK_LM_WG_PER_CU;
     if (per_cu < 1) per_cu = 1;

@@ -9,21 +9,22 @@
 // G = -log(-log(max(u, 2^-126))) with u = Triton's tl.rand(seed, v): Philox4x32-10 word 0
 // of counter (v, 0, 0, 0) under key (seed lo32, seed hi32).
 //
-// Design (MI355X): one workgroup of 256 threads per 8192-element slice of a row; each
-// thread holds 32 logits from eight coalesced 16-byte loads, so the logits are read from
-// HBM exactly once.  The Philox/log work is the expensive part (~150 VALU ops per element),
-// so the kernel prunes exactly instead of computing noise everywhere:
-//   * every thread first scores its own largest raw logit (one Philox each, in parallel);
-//     each slice publishes the best of those with a 64-bit atomicMax and waits (bounded
-//     in time, so it can never deadlock) until all slices of its row have published; the
-//     row's best candidate L is then a value the row's winner is >= to;
-//   * since G <= GUMBEL_MAX for every possible u, an element with
-//     fl(fl(x/T) + GUMBEL_MAX) < L can never win (rounding is monotone), and that test
-//     reduces to one compare of the raw logit against a per-row cutoff;
-//   * the surviving elements are compacted per wave through LDS and scored 64 at a time.
-// The per-row winner is merged with atomicMax on the key (orderable(y) << 32 | ~v), which
-// gives the largest y and, among equal y, the smallest v; the last slice of a row (an
-// atomic counter) writes out[b] and resets the row's workspace for the next launch.
+// Design (MI355X).  The Philox + two logs cost ~140 VALU instructions per element, so
+// scoring every element of a [32, 248320] batch is ALU-bound (~30 us).  The kernel prunes
+// exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
+// row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
+// A good L needs the whole row, so the work is two launches with no spinning or cross-
+// workgroup waits:
+//   1. gumbel_cand_kernel streams the logits (256 threads x 64 floats per workgroup,
+//      coalesced 16-byte loads); greedy rows finish their argmax here; sampled rows score
+//      one candidate per thread (its largest raw logit) and publish the workgroup's best
+//      with one 64-bit atomicMax on (orderable(y) << 32 | ~v) - largest y, then smallest v;
+//   2. gumbel_surv_kernel re-reads only the sampled rows' slices (recently streamed, so
+//      mostly served by the 256 MB last-level cache), drops everything under the row's
+//      cutoff with one compare, scores the survivors through a per-wave LDS queue in full
+//      64-lane batches, and the last slice of each row writes the token and clears the
+//      row's workspace for the next call.
+// On the BASELINE logits about 13% of a B=32 batch survives.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,7 +37,7 @@ namespace vqk {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int SMP_THREADS = 256;
-constexpr int SMP_EPT = 32;                               // elements per thread
+constexpr int SMP_EPT = 64;                               // elements per thread
 constexpr int SMP_CHUNK = SMP_THREADS * SMP_EPT;          // elements per workgroup
 constexpr float GREEDY_EPS = 1e-5f;
 
@@ -50,11 +51,9 @@ struct SmpArgs {
   const float* thr;
   int64_t* out;
   unsigned long long* keys;  // [B] row best key
-  unsigned int* arrive;      // [B] slices that published their candidates
-  unsigned int* done;        // [B] slices finished
+  unsigned int* done;        // [B] slices of the survivor launch finished
   int nchunks;
   int vec;                   // 16-byte loads allowed
-  uint64_t wait_ticks;       // bound of the wait for the row's other slices (wall clock)
   float* scores;             // debug: write y for every element (scores kernel only)
 };
 
@@ -111,12 +110,11 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 
 // Cross-workgroup protocol.  Only device-scope atomics on the workspace are used, relaxed:
 // acquire/release fences would write back and invalidate the L2 of the issuing XCD
-// (buffer_wbl2 / buffer_inv), which costs far more than the whole reduction.  Ordering that
-// matters is enforced by waiting for an atomic's return (s_waitcnt) before the next one:
-//  * a slice's key max is performed before its arrive/done increment is issued;
-//  * the last slice (the one whose done increment returns nchunks-1) reads the key after
-//    that increment returned, so it sees every slice's max.
-// Any key value read earlier is a real candidate's key, hence always a valid pruning bound.
+// (buffer_wbl2 / buffer_inv), which costs far more than the whole reduction.  The ordering
+// that matters is enforced by waiting for an atomic to complete (s_waitcnt) before the next:
+// a slice's key max is performed before its done increment is issued, so the slice whose
+// increment returns nchunks-1 reads a key that holds every slice's max.  The launch boundary
+// orders launch 1's atomics before launch 2.
 __device__ __forceinline__ unsigned long long ld_relaxed_u64(unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -131,165 +129,189 @@ __device__ __forceinline__ unsigned int aadd_u32(unsigned int* p, unsigned int v
 }
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-constexpr int QCAP = 128;  // per-wave survivor queue (entries)
 
-__global__ void __launch_bounds__(SMP_THREADS) gumbel_argmax_kernel(SmpArgs a) {
-  __shared__ unsigned long long red[SMP_THREADS / 64];
-  __shared__ float qx[SMP_THREADS / 64][QCAP];
-  __shared__ uint32_t qv[SMP_THREADS / 64][QCAP];
-  __shared__ unsigned long long row_best;
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long k, unsigned long long* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  k = wave_max_u64(k);
+  if (lane == 0) red[wave] = k;
+  __syncthreads();
+  unsigned long long r = red[0];
+#pragma unroll
+  for (int w = 1; w < SMP_THREADS / 64; ++w) r = (red[w] > r) ? red[w] : r;
+  return r;
+}
 
-  const int row = blockIdx.y;
-  const int chunk = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* rowp = a.logits + (int64_t)row * a.ld;
-  const int base = chunk * SMP_CHUNK;
-  const RowParams p = row_params(a, row);
-  const float NEG_INF = -__builtin_inff();
+// Branch-free running maximum on the order-preserving key (so NaN is the largest and
+// -0.0 == +0.0); a strict compare keeps the first, i.e. smallest, index.
+__device__ __forceinline__ void take_max(uint32_t k, int q, uint32_t& km, int& qm) {
+  const bool b = k > km;
+  km = b ? k : km;
+  qm = b ? q : qm;
+}
 
-  // ---- load 32 logits per thread (element e of load i sits at base + (i*256 + tid)*4 + e)
-  float x[SMP_EPT];
-  if (a.vec && base + SMP_CHUNK <= a.V) {
+// One thread's 64 logits of a slice, all loads issued before any is used.  Full slices
+// (16-byte aligned rows) take sixteen 16-byte loads; the row's last, ragged slice (or an
+// unaligned row) takes clamped scalar loads, always in bounds, masked by the caller.  The
+// two forms sit in separate branches around the whole batch of loads: a data-dependent
+// choice per load would make the compiler wait for each load before issuing the next.
+__device__ __forceinline__ int slice_v(int base, int tid, int q) {
+  return base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
+}
+__device__ __forceinline__ void load_slice(const float* rowp, int base, int tid, int V, bool full,
+                                           float (&xv)[SMP_EPT]) {
+  if (full) {
 #pragma unroll
     for (int i = 0; i < SMP_EPT / 4; ++i) {
-      v4f t = __builtin_nontemporal_load((const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4));
-      x[4 * i + 0] = t.x;
-      x[4 * i + 1] = t.y;
-      x[4 * i + 2] = t.z;
-      x[4 * i + 3] = t.w;
+      const v4f t = *(const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4);
+      xv[4 * i] = t.x;
+      xv[4 * i + 1] = t.y;
+      xv[4 * i + 2] = t.z;
+      xv[4 * i + 3] = t.w;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < SMP_EPT / 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        int v = base + (i * SMP_THREADS + tid) * 4 + e;
-        x[4 * i + e] = (v < a.V) ? rowp[v] : NEG_INF;
-      }
+    for (int q = 0; q < SMP_EPT; ++q) {
+      const int v = slice_v(base, tid, q);
+      xv[q] = rowp[v < V ? v : V - 1];
+    }
   }
-  auto vidx = [&](int q) -> uint32_t { return (uint32_t)(base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3)); };
-  auto valid = [&](int q) -> bool { return (int)vidx(q) < a.V; };
-  auto admissible = [&](int q) -> bool { return !(p.has_thr && !(x[q] >= p.thr)); };
+}
 
-  unsigned long long best = 0ull;  // below every real key
+// Launch 1 (streams every logit once): 256 threads x 64 floats per workgroup.  Greedy rows:
+// each thread keeps its argmax of y = (admissible ? x : -inf).  Sampled rows: each thread
+// keeps its largest admissible raw logit and scores it (one Philox per 64 elements); a thread
+// with no admissible element offers its first element as -inf.  The workgroup's best key goes
+// to the row with one fire-and-forget 64-bit atomicMax.
+__global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
+  __shared__ unsigned long long red[SMP_THREADS / 64];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const int base = blockIdx.x * SMP_CHUNK;
+  const bool full = a.vec && base + SMP_CHUNK <= a.V;
+  float xv[SMP_EPT];
+  load_slice(rowp, base, tid, a.V, full, xv);
+  const RowParams p = row_params(a, row);
+  const float NEG_INF = -__builtin_inff();
+  uint32_t km = 0u;  // below orderable(-inf)
+  int qm = -1;
+#pragma unroll
+  for (int q = 0; q < SMP_EPT; ++q) {
+    const bool in = slice_v(base, tid, q) < a.V;
+    const bool adm = !(p.has_thr && !(xv[q] >= p.thr));
+    // greedy: y itself; sampled: the raw logit ranks the candidates (inadmissible as -inf)
+    const uint32_t k = in ? orderable(adm ? xv[q] : NEG_INF) : 0u;
+    take_max(k, q, km, qm);
+  }
+  unsigned long long best = 0ull;
+  if (qm >= 0) {
+    const uint32_t v = (uint32_t)slice_v(base, tid, qm);
+    float y = from_orderable(km);
+    if (!p.greedy && y > NEG_INF) y = score(p, y, v);
+    best = make_key(y, v);
+  }
+  const unsigned long long gb = block_max_u64(best, red);
+  if (tid == 0) amax_u64(&a.keys[row], gb);
+}
+
+// Launch 2.  Greedy rows: slice 0 writes the token.  Sampled rows: the row key holds every
+// slice's candidate, a value L the winner is >= to.  Since G <= GUMBEL_MAX for every Philox
+// word and rounding is monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is
+// one compare against a per-row raw-logit cutoff.  The slice's 64 floats per thread are
+// loaded at once; survivors are appended to a per-wave LDS queue (ballot + popcount) and
+// scored in full-wave batches of 128, two per lane (independent chains).  The last slice of
+// the row (per-row counter) writes the token and clears the row's workspace.
+constexpr int SURV_GROUP = 16;                     // elements appended between queue drains
+constexpr int QCAP = 128 + SURV_GROUP * 64;        // per-wave queue entries
+
+__device__ __forceinline__ void drain128(const RowParams& p, float* qx, uint32_t* qv, int& qn, int lane,
+                                         unsigned long long& best) {
+  while (qn >= 128) {
+    qn -= 128;
+    const float x0 = qx[qn + lane], x1 = qx[qn + 64 + lane];
+    const uint32_t v0 = qv[qn + lane], v1 = qv[qn + 64 + lane];
+    const unsigned long long k0 = make_key(score(p, x0, v0), v0);
+    const unsigned long long k1 = make_key(score(p, x1, v1), v1);
+    best = (k0 > best) ? k0 : best;
+    best = (k1 > best) ? k1 : best;
+  }
+}
+
+__global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
+  __shared__ unsigned long long red[SMP_THREADS / 64];
+  __shared__ float qxs[SMP_THREADS / 64][QCAP];
+  __shared__ uint32_t qvs[SMP_THREADS / 64][QCAP];
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const RowParams p = row_params(a, row);
   if (p.greedy) {
-#pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
-      if (!valid(q)) continue;
-      float y = admissible(q) ? x[q] : NEG_INF;
-      unsigned long long k = make_key(y, vidx(q));
-      best = (k > best) ? k : best;
-    }
-  } else {
-    // 1) each thread scores its largest admissible raw logit (ties -> smallest index);
-    //    inadmissible elements still compete as -inf, as in the reference's masking
-    int qm = -1;
-    float xm = NEG_INF;
-#pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
-      if (!valid(q)) continue;
-      if (!admissible(q)) {
-        unsigned long long k = make_key(NEG_INF, vidx(q));
-        best = (k > best) ? k : best;
-      } else if (qm < 0 || x[q] > xm) {
-        qm = q;
-        xm = x[q];
-      }
-    }
-    if (qm >= 0) {
-      unsigned long long k = make_key(score(p, xm, vidx(qm)), vidx(qm));
-      best = (k > best) ? k : best;
-    }
-    // 2) publish this slice's best to the row; wait (bounded) until every slice of the
-    //    row has published, so the pruning bound below is the row-wide one.  The wait
-    //    only affects speed: the pruning is exact with whatever bound is visible.
-    unsigned long long wb = wave_max_u64(best);
-    if (lane == 0) red[wave] = wb;
-    __syncthreads();
-    if (tid == 0) {
-      unsigned long long gb = red[0];
-#pragma unroll
-      for (int w = 1; w < SMP_THREADS / 64; ++w) gb = (red[w] > gb) ? red[w] : gb;
-      amax_u64(&a.keys[row], gb);
-      wait_vmem();
-      aadd_u32(&a.arrive[row], 1u);
-      const uint64_t t0 = wall_clock64();
-      while (ld_relaxed_u32(&a.arrive[row]) < (unsigned int)a.nchunks && wall_clock64() - t0 < a.wait_ticks)
-        __builtin_amdgcn_s_sleep(8);
-      row_best = ld_relaxed_u64(&a.keys[row]);
-    }
-    __syncthreads();
-    const unsigned long long lk = row_best;
-    const float L = from_orderable((uint32_t)(lk >> 32));
-    // 3) raw-logit cutoff xc with fl(fl(xc/T) + GUMBEL_MAX) < L; elements with x <= xc
-    //    cannot reach L (G <= GUMBEL_MAX for every Philox word; rounding is monotone)
-    float xc = NEG_INF;
-    if (L > NEG_INF && L == L) {
-      float c = (L - GUMBEL_MAX) * p.T;
-      for (int it = 0; it < 16; ++it) {
-        if ((c / p.T) + GUMBEL_MAX < L) {
-          xc = c;
-          break;
-        }
-        c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
-      }
-    }
-    // 4) score the survivors through a per-wave queue: full 64-lane batches of Philox work
-    //    instead of mostly-masked lanes
-    int qn = 0;
-#pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
-      const bool s = valid(q) && q != qm && admissible(q) && !(x[q] <= xc);
-      const unsigned long long m = __ballot(s);
-      if (m == 0ull) continue;
-      const int pos = qn + __popcll(m & ((1ull << lane) - 1ull));
-      if (s) {
-        qx[wave][pos] = x[q];
-        qv[wave][pos] = vidx(q);
-      }
-      qn += __popcll(m);
-      __builtin_amdgcn_wave_barrier();
-      if (qn >= 64) {
-        const float xv = qx[wave][lane];
-        const uint32_t v = qv[wave][lane];
-        const float xr = (qn - 64 > lane) ? qx[wave][64 + lane] : 0.f;
-        const uint32_t vr = (qn - 64 > lane) ? qv[wave][64 + lane] : 0u;
-        __builtin_amdgcn_wave_barrier();
-        if (qn - 64 > lane) {
-          qx[wave][lane] = xr;
-          qv[wave][lane] = vr;
-        }
-        qn -= 64;
-        const unsigned long long k = make_key(score(p, xv, v), v);
-        best = (k > best) ? k : best;
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    if (lane < qn) {
-      const float xv = qx[wave][lane];
-      const uint32_t v = qv[wave][lane];
-      const unsigned long long k = make_key(score(p, xv, v), v);
-      best = (k > best) ? k : best;
-    }
-  }
-
-  // ---- workgroup reduce, merge into the row, last slice writes the token and resets
-  unsigned long long wb = wave_max_u64(best);
-  if (lane == 0) red[wave] = wb;
-  __syncthreads();
-  if (tid == 0) {
-    unsigned long long gb = red[0];
-#pragma unroll
-    for (int w = 1; w < SMP_THREADS / 64; ++w) gb = (red[w] > gb) ? red[w] : gb;
-    amax_u64(&a.keys[row], gb);
-    wait_vmem();
-    unsigned int d = aadd_u32(&a.done[row], 1u);
-    if (d == (unsigned int)(a.nchunks - 1)) {
-      // every other slice's max was performed before its done increment
-      unsigned long long k = amax_u64(&a.keys[row], 0ull);
+    if (blockIdx.x == 0 && tid == 0) {
+      const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
       a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
       __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const int base = blockIdx.x * SMP_CHUNK;
+  const bool full = a.vec && base + SMP_CHUNK <= a.V;
+  float xv[SMP_EPT];
+  load_slice(rowp, base, tid, a.V, full, xv);
+  const float NEG_INF = -__builtin_inff();
+  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
+  const float L = from_orderable((uint32_t)(lk >> 32));
+  float xc = NEG_INF;
+  if (L > NEG_INF && L == L) {
+    float c = (L - GUMBEL_MAX) * p.T;
+    for (int it = 0; it < 16; ++it) {
+      if ((c / p.T) + GUMBEL_MAX < L) {
+        xc = c;
+        break;
+      }
+      c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
+    }
+  }
+  float* qx = qxs[wave];
+  uint32_t* qv = qvs[wave];
+  unsigned long long best = 0ull;
+  int qn = 0;
+#pragma unroll
+  for (int g0 = 0; g0 < SMP_EPT; g0 += SURV_GROUP) {
+#pragma unroll
+    for (int q = g0; q < g0 + SURV_GROUP; ++q) {
+      const int v = slice_v(base, tid, q);
+      const bool s = v < a.V && !(p.has_thr && !(xv[q] >= p.thr)) && !(xv[q] <= xc);
+      const unsigned long long m = __ballot(s);
+      const int pos = qn + __popcll(m & ((1ull << lane) - 1ull));
+      if (s) {
+        qx[pos] = xv[q];
+        qv[pos] = (uint32_t)v;
+      }
+      qn += __popcll(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    drain128(p, qx, qv, qn, lane, best);
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (lane < qn) {
+    const float x0 = qx[lane];
+    const uint32_t v0 = qv[lane];
+    const bool has1 = lane + 64 < qn;
+    const float x1 = has1 ? qx[lane + 64] : x0;
+    const uint32_t v1 = has1 ? qv[lane + 64] : v0;
+    const unsigned long long k0 = make_key(score(p, x0, v0), v0);
+    const unsigned long long k1 = make_key(score(p, x1, v1), v1);
+    best = (k0 > best) ? k0 : best;
+    best = (k1 > best) ? k1 : best;
+  }
+  const unsigned long long gb = block_max_u64(best, red);
+  if (tid == 0) {
+    if (gb > lk) amax_u64(&a.keys[row], gb);
+    wait_vmem();
+    const unsigned int d = aadd_u32(&a.done[row], 1u);
+    if (d == (unsigned int)(a.nchunks - 1)) {
+      // every other slice's max was performed before its done increment returned
+      const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
+      a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
+      __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&a.done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -310,23 +332,7 @@ using namespace vqk;
 
 extern "C" int64_t vqk_gumbel_workspace_size(int64_t B) {
   if (B < 0) return 0;
-  return B * (int64_t)(sizeof(unsigned long long) + 2 * sizeof(unsigned int)) + 16;
-}
-
-// Wall-clock ticks per microsecond of the current device (the counter wall_clock64 reads).
-static uint64_t ticks_per_us() {
-  static thread_local int dev_cached = -1;
-  static thread_local uint64_t tpu = 100;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return tpu;
-  if (dev != dev_cached) {
-    int khz = 0;
-    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz > 0)
-      tpu = (uint64_t)khz / 1000u;
-    if (tpu == 0) tpu = 1;
-    dev_cached = dev;
-  }
-  return tpu;
+  return B * (int64_t)(sizeof(unsigned long long) + sizeof(unsigned int)) + 16;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
@@ -358,12 +364,12 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.thr = topk_thr;
   a.out = out;
   a.keys = (unsigned long long*)workspace;
-  a.arrive = (unsigned int*)((char*)workspace + B * sizeof(unsigned long long));
-  a.done = a.arrive + B;
-  a.wait_ticks = 8 * ticks_per_us();
+  a.done = (unsigned int*)((char*)workspace + B * sizeof(unsigned long long));
   a.nchunks = (int)((V + SMP_CHUNK - 1) / SMP_CHUNK);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
-  hipLaunchKernelGGL(gumbel_argmax_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+  hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+                     (hipStream_t)stream, a);
+  hipLaunchKernelGGL(gumbel_surv_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                      (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;

@@ -4,9 +4,10 @@ The library is built in-tree by ``csrc/build.py`` (``__graft_entry__.build()``) 
 next to this file.  There is no fallback: if the library or a gfx950 device is missing,
 every entry point raises, so a run that produces numbers has run the HIP kernels.
 
-Error mapping (mirrors the reference's contract): argument problems detected
-before launch raise ``ValueError`` (``AssertionError`` is used by the Python wrappers for
-the reference's own asserts); launch failures raise ``RuntimeError``.
+Error mapping (mirrors the reference's contract, src/vllm_quant_kernels/_sampler_kernels.py:
+148-156 and _quant.py:47, 78-79): argument problems detected before launch raise
+``ValueError`` (``AssertionError`` is used by the Python wrappers for the reference's own
+asserts); launch failures raise ``RuntimeError``.
 """
 from __future__ import annotations
 
