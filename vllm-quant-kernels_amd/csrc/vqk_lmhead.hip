@@ -49,7 +49,7 @@
 #define VQK_LM_LDS 1       // stage weights through LDS with direct-to-LDS loads when K allows
 #endif
 #ifndef VQK_LM_LDS_STAGES
-#define VQK_LM_LDS_STAGES 2  // LDS ring depth per wave (4 KB stages)
+#define VQK_LM_LDS_STAGES 4  // LDS ring depth per wave (4 KB stages) when LDS allows, else 2
 #endif
 #ifndef VQK_LM_LDS_WG_PER_CU
 #define VQK_LM_LDS_WG_PER_CU 1
@@ -122,13 +122,20 @@ struct LmArgs {
   int M, K, Bg, Ball;
   int out_vec;          // 1 when 8-byte output stores are aligned
   float xs_val;         // W8A8 with pre-quantized activations: the per-tensor scale
-  int lds_x_bytes;      // LDS-staged variant: bytes of the activation fragments (16-aligned)
+  int lds_x_bytes;      // LDS bytes of the staged activations (fragments + MX scales), 16-aligned
+  int xr;               // LDS bytes per batch row of fragments (16 * odd)
+  int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
+  int xs_off;           // MX: LDS byte offset of the activation scales
 };
 
 // ---------------------------------------------------------------------------------------
-// Prologue: stage the activations of this batch group into LDS in fragment order.
-// Fragment (mi, g, b) lives at byte ((mi*4 + g) * Bg + b) * FB; a zero fragment follows.
-// MX scales: dword ((mi/4)*4 + g) * Bg + b holds byte (mi % 4) for fragment mi.
+// Prologue: stage the activations of this batch group into LDS in fragment order, one
+// batch row after the other: fragment (mi, g) of row b lives at byte b*xr + (mi*4 + g)*FB, so
+// consecutive MFMAs of a lane are a constant 4*FB apart.  xr/16 is odd, which puts the 16
+// rows a ds_read_b128 serves in one pass on 16 different bank groups.
+// MX scales: dword xs_off/4 + b*xsr + (mi/4)*4 + g holds byte (mi % 4) for fragment mi.
+// Lanes of columns b >= Bg read row Bg-1 (their results are never stored), so no zero
+// fragments are needed.
 template <int MODE, int DT>
 __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
   typedef ModeTraits<MODE> T;
@@ -136,8 +143,6 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
   const int K = a.K, Bg = a.Bg;
   const int NMF = K / T::KPM;  // MFMAs per row
   const int nfrag = NMF * 4 * Bg;
-  uint8_t* zero = lds + (size_t)nfrag * T::FB;
-  for (int i = tid; i < T::FB / 4; i += nth) ((uint32_t*)zero)[i] = 0u;
 
   float xs_w8a8 = a.xs_val;
   if (MODE == M_W8A8 && !a.xq) {
@@ -194,11 +199,11 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
         sbyte = (uint32_t)(kx + 127);
       }
       const int g0 = 2 * (j & 1), off = 16 * (j >> 1);
-      uint8_t* d0 = lds + (size_t)((mi * 4 + g0) * Bg + b) * T::FB + off;
-      uint8_t* d1 = lds + (size_t)((mi * 4 + g0 + 1) * Bg + b) * T::FB + off;
+      uint8_t* d0 = lds + (size_t)b * a.xr + (size_t)(mi * 4 + g0) * T::FB + off;
+      uint8_t* d1 = d0 + T::FB;
       *(uint4*)d0 = make_uint4(v[0], v[1], v[2], v[3]);
       *(uint4*)d1 = make_uint4(v[4], v[5], v[6], v[7]);
-      uint8_t* sdst = (uint8_t*)(lds_xs + ((size_t)((mi >> 2) * 4 + j) * Bg + b)) + (mi & 3);
+      uint8_t* sdst = (uint8_t*)(lds_xs + (size_t)b * a.xsr + (mi >> 2) * 4 + j) + (mi & 3);
       *sdst = (uint8_t)sbyte;
     }
   } else {
@@ -206,7 +211,7 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
       const int b = f % Bg;
       const int gm = f / Bg;
       const int g = gm & 3, mi = gm >> 2;
-      uint8_t* dst = lds + (size_t)f * T::FB;
+      uint8_t* dst = lds + (size_t)b * a.xr + (size_t)gm * T::FB;
       if (MODE == M_W8A16) {
         const uint16_t* src = (const uint16_t*)a.x + (int64_t)b * a.ldx + frag_k<MODE>(mi, g, 0);
         uint32_t v[4];
@@ -242,11 +247,6 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
         if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
       }
     }
-  }
-  if (T::MX) {
-    // padding lanes (b >= Bg) read this dword: scale 1.0 (byte 127) in every position
-    const int nsd = ((NMF + 3) / 4) * 4 * Bg;
-    if (tid == 0) lds_xs[nsd] = 0x7F7F7F7Fu;
   }
   __syncthreads();
 }
@@ -328,18 +328,33 @@ struct Acc {
   __device__ __forceinline__ void zero(int ct) { v[ct] = (typename AccT<MODE>::type)(0); }
 };
 
-// B-operand LDS byte offset for MFMA mi, lane (g, j), column tile ct.
-template <int MODE>
-__device__ __forceinline__ uint32_t frag_off(int mi, int g, int b, int Bg, uint32_t zero_off) {
+// Per-lane activation pointers: xb[ct] = fragment (mi = 0, g) of column b = ct*16 + j
+// (clamped to Bg-1), xsb[ct] = its MX scale dword for mi = 0.  Fragment mi is 4*FB*mi
+// bytes further, its scale dword 4*(mi/4) dwords further.
+template <int MODE, int NCT>
+struct XPtr {
+  const uint8_t* xb[NCT];
+  const uint32_t* xsb[NCT];
+};
+template <int MODE, int NCT>
+__device__ __forceinline__ XPtr<MODE, NCT> x_pointers(const LmArgs& a, const uint8_t* lds, const uint32_t* lds_xs,
+                                                      int g, int j) {
   typedef ModeTraits<MODE> T;
-  return (b < Bg) ? (uint32_t)(((mi * 4 + g) * Bg + b) * T::FB) : zero_off;
+  XPtr<MODE, NCT> p;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int b = (ct * 16 + j < a.Bg) ? ct * 16 + j : a.Bg - 1;
+    p.xb[ct] = lds + b * a.xr + g * T::FB;
+    p.xsb[ct] = lds_xs + b * a.xsr + g;
+  }
+  return p;
 }
 
 template <int MODE, int NCT>
 __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MODE>& s, int c, int g,
-                                              int j, int Bg, const uint8_t* lds, uint32_t zero_off,
-                                              const uint32_t* lds_xs, uint32_t xs_pad_idx) {
+                                              const XPtr<MODE, NCT>& xp) {
   typedef ModeTraits<MODE> T;
+  constexpr int XS = 4 * T::FB;  // bytes between consecutive fragments of a lane
   if constexpr (MODE == M_W8A16) {
     uint32_t d[8] = {(uint32_t)s.lo.x, (uint32_t)s.lo.y, (uint32_t)s.lo.z, (uint32_t)s.lo.w,
                      (uint32_t)s.hi.x, (uint32_t)s.hi.y, (uint32_t)s.hi.z, (uint32_t)s.hi.w};
@@ -352,7 +367,7 @@ __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MO
       const int mi = 4 * c + m;
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
-        v8h Bv = *(const v8h*)(lds + frag_off<MODE>(mi, g, ct * 16 + j, Bg, zero_off));
+        v8h Bv = *(const v8h*)(xp.xb[ct] + mi * XS);
         acc.v[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bv, acc.v[ct], 0, 0, 0);
       }
     }
@@ -363,7 +378,7 @@ __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MO
       const int mi = 2 * c + h;
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
-        v4i Bv = *(const v4i*)(lds + frag_off<MODE>(mi, g, ct * 16 + j, Bg, zero_off));
+        v4i Bv = *(const v4i*)(xp.xb[ct] + mi * XS);
         acc.v[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc.v[ct], 0, 0, 0);
       }
     }
@@ -374,15 +389,11 @@ __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MO
     if (MODE == M_MXFP8) sa = (int)(s.s0 >> (8 * g));
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
-      const int b = ct * 16 + j;
-      const v4i* bp = (const v4i*)(lds + frag_off<MODE>(mi, g, b, Bg, zero_off));
+      const v4i* bp = (const v4i*)(xp.xb[ct] + mi * XS);
       v4i b0 = bp[0], b1 = bp[1];
       v8i Bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
       int sb = 127;
-      if (MODE == M_MXFP8) {
-        uint32_t di = (b < Bg) ? (uint32_t)(((mi >> 2) * 4 + g) * Bg + b) : xs_pad_idx;
-        sb = (int)(lds_xs[di] >> (8 * (mi & 3)));
-      }
+      if (MODE == M_MXFP8) sb = (int)(xp.xsb[ct][(mi >> 2) * 4] >> (8 * (mi & 3)));
       acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc.v[ct], 0, 0, 0, sa, 0, sb);
     }
   } else {  // MXFP4: two MFMAs per chunk, A = 32 E2M1 values (16 bytes) per lane
@@ -396,12 +407,10 @@ __device__ __forceinline__ void compute_chunk(Acc<MODE, NCT>& acc, const Slot<MO
       int sa = (int)((h ? s.s1 : s.s0) >> (8 * g));
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
-        const int b = ct * 16 + j;
-        const v4i* bp = (const v4i*)(lds + frag_off<MODE>(mi, g, b, Bg, zero_off));
+        const v4i* bp = (const v4i*)(xp.xb[ct] + mi * XS);
         v4i b0 = bp[0], b1 = bp[1];
         v8i Bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-        uint32_t di = (b < Bg) ? (uint32_t)(((mi >> 2) * 4 + g) * Bg + b) : xs_pad_idx;
-        int sb = (int)(lds_xs[di] >> (8 * (mi & 3)));
+        int sb = (int)(xp.xsb[ct][(mi >> 2) * 4] >> (8 * (mi & 3)));
         acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc.v[ct], 4, 0, 0, sa, 0, sb);
       }
     }
@@ -494,13 +503,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
   __shared__ float red[17];
   const int K = a.K;
   const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;  // weight bytes per row
-  const int NMF = K / T::KPM;
-  const int Bg = a.Bg;
-  const uint32_t frag_bytes = (uint32_t)NMF * 4 * Bg * T::FB;
   uint8_t* lds = smem;
-  uint32_t* lds_xs = (uint32_t*)(smem + frag_bytes + T::FB);
-  const uint32_t zero_off = frag_bytes;
-  const uint32_t xs_pad_idx = (uint32_t)((NMF + 3) / 4) * 4 * Bg;
+  uint32_t* lds_xs = (uint32_t*)(smem + a.xs_off);
 
   stage_x<MODE>(a, lds, lds_xs, red);
   const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
@@ -509,6 +513,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
   const int wave = threadIdx.x >> 6;
   const int nwaves = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
+  const XPtr<MODE, NCT> xp = x_pointers<MODE, NCT>(a, lds, lds_xs, g, r);
   const int ntiles = (a.M + 15) >> 4;
   const int wid = blockIdx.x * nwaves + wave;
   const int total = gridDim.x * nwaves;
@@ -552,7 +557,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
     row_ptrs(tqn, rpn, spn);
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      compute_chunk<MODE, NCT>(acc, ring[d], c0 + d, g, r, Bg, lds, zero_off, lds_xs, xs_pad_idx);
+      compute_chunk<MODE, NCT>(acc, ring[d], c0 + d, g, xp);
       load_chunk<MODE>(ring[d], rpn, spn, cn0 + d, g);
       // keep each chunk's LDS reads next to its MFMAs: hoisting them across chunks only
       // raises register pressure (and occupancy is what hides the HBM latency here)
@@ -623,41 +628,59 @@ __device__ __forceinline__ void select_tile_scales(const uint32_t (&sdw)[16], in
   }
 }
 
+// One stage of a wave: 256 weight bytes of each of its tile's 16 rows (4 KB, rows rotated as
+// described above), then for MX modes the rows' E8M0 scales of those bytes (16 x 8 B for
+// MXFP8, 16 x 16 B for MXFP4).  Weights and scales arrive by the same direct-to-LDS loads,
+// so one vmcnt wait covers the whole stage.
 template <int MODE>
-struct StageScales {  // MX scale dwords of one stage (2 chunks): MXFP8 2, MXFP4 4
-  uint32_t d[4];
+struct StageGeom {
+  static constexpr int SB = (MODE == M_MXFP8) ? 8 : (MODE == M_MXFP4) ? 16 : 0;  // scale bytes/row
+  static constexpr int SLOT = LDS_STAGE + 16 * SB;
+  static constexpr int NV = 4 + (SB ? 1 : 0);  // vector-memory instructions per stage
 };
 
+// Per-lane byte offsets, relative to the tile's first row, of the 4 weight pieces and of the
+// scale piece this lane fetches for tile t (rows past M are clamped to M-1).
 template <int MODE>
-__device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int tile, int ks, uint8_t* slot, int lane,
-                                            StageScales<MODE>& sc) {
-  typedef ModeTraits<MODE> T;
-  const int rr = lane >> 4;            // row within the instruction's 4
-  const int pp = 16 * (lane & 15);     // byte position within the row's 256 in LDS
+struct IssueOffsets {
+  uint32_t w[4];
+  uint32_t s;
+};
+template <int MODE>
+__device__ __forceinline__ void issue_offsets(const LmArgs& a, int KB, int t, int lane, IssueOffsets<MODE>& o) {
+  const int rr = lane >> 4, pp = 16 * (lane & 15);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * i + rr;
-    int m = tile * 16 + row;
-    m = (m < a.M) ? m : (a.M - 1);
-    const int c = (pp - 16 * row) & 255;  // global byte of the row stored at position pp
-    const uint8_t* src = a.w + (int64_t)m * KB + 256 * ks + c;
-    __builtin_amdgcn_global_load_lds(VQK_GPTR(src), VQK_LPTR(slot + 1024 * i), 16, 0, VQK_LM_NT_LDS);
+    const int m = min(16 * t + row, a.M - 1);
+    o.w[i] = (uint32_t)((m - 16 * t) * KB + ((pp - 16 * row) & 255));
   }
-  if constexpr (T::MX) {
-    int m = tile * 16 + (lane & 15);
-    m = (m < a.M) ? m : (a.M - 1);
-    const uint32_t* srow = (const uint32_t*)((const uint8_t*)a.ws + (int64_t)m * (a.K >> 5));
-    if constexpr (MODE == M_MXFP8) {
-      typedef int v2i __attribute__((ext_vector_type(2)));
-      v2i t = *(const v2i*)(srow + 2 * ks);
-      sc.d[0] = (uint32_t)t.x;
-      sc.d[1] = (uint32_t)t.y;
+  if constexpr (MODE == M_MXFP8) {  // lanes 0..31: row lane/2, dword lane%2 of its 8 bytes
+    const int m = min(16 * t + ((lane >> 1) & 15), a.M - 1);
+    o.s = (uint32_t)((m - 16 * t) * (a.K >> 5) + 4 * (lane & 1));
+  } else if constexpr (MODE == M_MXFP4) {  // lanes 0..15: row lane, 16 bytes
+    const int m = min(16 * t + (lane & 15), a.M - 1);
+    o.s = (uint32_t)((m - 16 * t) * (a.K >> 5));
+  } else {
+    o.s = 0;
+  }
+}
+template <int MODE>
+__device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int ks, uint8_t* slot, int lane,
+                                            const IssueOffsets<MODE>& o) {
+  typedef StageGeom<MODE> G;
+  const uint8_t* tb = a.w + (int64_t)t * 16 * KB + 256 * ks;  // wave-uniform
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __builtin_amdgcn_global_load_lds(VQK_GPTR(tb + o.w[i]), VQK_LPTR(slot + 1024 * i), 16, 0, VQK_LM_NT_LDS);
+  if constexpr (G::SB > 0) {
+    const uint8_t* sb = (const uint8_t*)a.ws + (int64_t)t * 16 * (a.K >> 5) + G::SB * ks;
+    if (MODE == M_MXFP8) {
+      if (lane < 32)
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 4, 0, VQK_LM_NT_LDS);
     } else {
-      v4i t = *(const v4i*)(srow + 4 * ks);
-      sc.d[0] = (uint32_t)t.x;
-      sc.d[1] = (uint32_t)t.y;
-      sc.d[2] = (uint32_t)t.z;
-      sc.d[3] = (uint32_t)t.w;
+      if (lane < 16)
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 16, 0, VQK_LM_NT_LDS);
     }
   }
 }
@@ -665,66 +688,79 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int tile, i
 template <int MODE, int NCT, int S>
 __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
   typedef ModeTraits<MODE> T;
+  typedef StageGeom<MODE> G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float red[17];
-  constexpr int NV = 4 + (T::MX ? 1 : 0);  // vector-memory ops per stage
   const int K = a.K;
   const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;
-  const int NMF = K / T::KPM;
-  const int Bg = a.Bg;
-  const uint32_t frag_bytes = (uint32_t)NMF * 4 * Bg * T::FB;
   uint8_t* lds = smem;
-  uint32_t* lds_xs = (uint32_t*)(smem + frag_bytes + T::FB);
-  const uint32_t zero_off = frag_bytes;
-  const uint32_t xs_pad_idx = (uint32_t)((NMF + 3) / 4) * 4 * Bg;
-  const uint32_t x_bytes = (uint32_t)a.lds_x_bytes;
+  uint32_t* lds_xs = (uint32_t*)(smem + a.xs_off);
 
   stage_x<MODE>(a, lds, lds_xs, red);
   const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
-  const int nwaves = blockDim.x >> 6;
   const int r = lane & 15, g = lane >> 4;
+  const XPtr<MODE, NCT> xp = x_pointers<MODE, NCT>(a, lds, lds_xs, g, r);
   const int ntiles = (a.M + 15) >> 4;
-  const int wid = blockIdx.x * nwaves + wave;
-  const int total = gridDim.x * nwaves;
+  const int wid = blockIdx.x * 4 + wave;
+  const int total = gridDim.x * 4;
   if (wid >= ntiles) return;
   const int my_tiles = (ntiles - 1 - wid) / total + 1;
   const int SPT = KB >> 8;  // stages per tile (KB % 256 == 0, host guarantees)
   const int nst = my_tiles * SPT;
-  uint8_t* ring = smem + x_bytes + (uint32_t)wave * S * LDS_STAGE;
+  uint8_t* ring = smem + a.lds_x_bytes + wave * (S * G::SLOT);
 
-  StageScales<MODE> sc[S];
+  // lane (r, g) reads row r: its 4 pieces of a stage, rotated by 16r within the row's 256 B
+  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
+  const uint8_t* wpc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wpc[i] = ring + rbase + ((64 * i + 16 * g + 16 * r) & 255);
+  const uint8_t* spc = ring + LDS_STAGE + G::SB * r;  // MX: row r's scale bytes of a stage
+
+  // issue side: stage iq of the wave = (itile, iks)
+  IssueOffsets<MODE> io;
+  int itile = wid, iks = 0, iq = 0;
+  issue_offsets<MODE>(a, KB, itile, lane, io);
+  auto advance_issue = [&]() {
+    ++iq;
+    if (++iks == SPT) {
+      iks = 0;
+      itile += total;
+      if (iq < nst) issue_offsets<MODE>(a, KB, itile, lane, io);
+    }
+  };
 #pragma unroll
   for (int s0 = 0; s0 < S; ++s0) {
-    const int q = s0 < nst ? s0 : 0;
-    issue_stage<MODE>(a, KB, wid + (q / SPT) * total, q % SPT, ring + s0 * LDS_STAGE, lane, sc[s0]);
+    if (iq < nst) {
+      issue_stage<MODE>(a, KB, itile, iks, ring + s0 * G::SLOT, lane, io);
+      advance_issue();
+    }
   }
+
   Acc<MODE, NCT> acc;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
-  // lane (r, g) reads row r: base of the row in a slot and its rotation
-  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
-  const int rot = 16 * r;
   uint32_t sdw[16];  // the tile's row-scale dwords (wave-uniform), fetched at its first stage
+  int ctile = wid, cks = 0;
 
   for (int q0 = 0; q0 < nst; q0 += S) {
 #pragma unroll
     for (int s0 = 0; s0 < S; ++s0) {
       const int q = q0 + s0;
       if (q < nst) {
-        wait_vmcnt<(S - 1) * NV>();
-        const uint8_t* slot = ring + s0 * LDS_STAGE + rbase;
-        const int tq = q / SPT, ks = q - tq * SPT;
-        const int tile = wid + tq * total;
-        const bool tile_full = tile * 16 + 16 <= a.M;
-        if (T::ROWSCALE && ks == 0 && tile_full) tile_scales_smem<MODE>(a, tile, sdw);
+        // stage q has landed once at most the stages issued after it are outstanding
+        if (iq == q + S) wait_vmcnt<(S - 1) * G::NV>();
+        else wait_vmcnt<0>();
+        const bool tile_full = ctile * 16 + 16 <= a.M;
+        if (T::ROWSCALE && cks == 0 && tile_full) tile_scales_smem<MODE>(a, ctile, sdw);
+        const int so = s0 * G::SLOT;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
           Slot<MODE> st;
-          const v4i lo = *(const v4i*)(slot + ((128 * cc + 16 * g + rot) & 255));
-          const v4i hi = *(const v4i*)(slot + ((128 * cc + 64 + 16 * g + rot) & 255));
+          const v4i lo = *(const v4i*)(wpc[2 * cc] + so);
+          const v4i hi = *(const v4i*)(wpc[2 * cc + 1] + so);
           if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
             st.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           } else {
@@ -732,31 +768,38 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
             st.hi = hi;
           }
           if constexpr (MODE == M_MXFP8) {
-            st.s0 = sc[s0].d[cc];
+            st.s0 = *(const uint32_t*)(spc + so + 4 * cc);
           } else if constexpr (MODE == M_MXFP4) {
-            st.s0 = sc[s0].d[2 * cc];
-            st.s1 = sc[s0].d[2 * cc + 1];
+            typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+            const v2u t2 = *(const v2u*)(spc + so + 8 * cc);
+            st.s0 = t2.x;
+            st.s1 = t2.y;
           }
-          compute_chunk<MODE, NCT>(acc, st, 2 * ks + cc, g, r, Bg, lds, zero_off, lds_xs, xs_pad_idx);
+          compute_chunk<MODE, NCT>(acc, st, 2 * cks + cc, g, xp);
         }
-        if (ks == SPT - 1) {
+        if (cks == SPT - 1) {
           float tsc[4];
           if (!T::ROWSCALE) {
             tsc[0] = tsc[1] = tsc[2] = tsc[3] = 1.f;
           } else if (tile_full) {
             uint32_t raw[4];
             select_tile_scales<MODE>(sdw, g, raw);
-            row_scales_from_bits<MODE>(a, tile * 16, lane, raw, tsc);
+            row_scales_from_bits<MODE>(a, ctile * 16, lane, raw, tsc);
           } else {
-            row_scales<MODE>(a, tile * 16, lane, tsc);  // the ragged last tile
+            row_scales<MODE>(a, ctile * 16, lane, tsc);  // the ragged last tile
           }
-          epilogue<MODE, NCT>(acc, a, tile * 16, lane, xs_w8a8, tsc);
+          epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc);
+        }
+        if (++cks == SPT) {
+          cks = 0;
+          ctile += total;
         }
         // the slot's ds_reads have completed before the DMA refill may overwrite it
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        // refill this slot with stage q + S (the DMA waits for this slot's reads: lgkmcnt)
-        const int qn = q + S < nst ? q + S : q;
-        issue_stage<MODE>(a, KB, wid + (qn / SPT) * total, qn % SPT, ring + s0 * LDS_STAGE, lane, sc[s0]);
+        if (iq < nst) {
+          issue_stage<MODE>(a, KB, itile, iks, ring + so, lane, io);
+          advance_issue();
+        }
       }
     }
   }
@@ -797,12 +840,37 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
 }
 
 template <int MODE, int NCT>
-static int launch_lds(const LmArgs& a, size_t lds_bytes, int grid, hipStream_t st) {
+static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, hipStream_t st) {
   // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
-  hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, VQK_LM_LDS_STAGES>), dim3(grid), dim3(256), lds_bytes, st, a);
+  if (stages == 4)
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4>), dim3(grid), dim3(256), lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 2>), dim3(grid), dim3(256), lds_bytes, st, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }
+
+// LDS layout of the staged activations (see stage_x_dt): fragment rows of xr bytes with
+// xr/16 odd, then for MX modes scale rows of xsr dwords with xsr odd.
+template <int MODE>
+struct XLayout {
+  int xr, xsr;
+  static XLayout make(int64_t K) {
+    typedef ModeTraits<MODE> T;
+    XLayout l;
+    const int NMF = (int)(K / T::KPM);
+    l.xr = NMF * 4 * T::FB;
+    if (((l.xr / 16) & 1) == 0) l.xr += 16;
+    l.xsr = 0;
+    if (T::MX) {
+      l.xsr = ((NMF + 3) / 4) * 4;
+      if ((l.xsr & 1) == 0) l.xsr += 1;
+    }
+    return l;
+  }
+  size_t per_row() const { return (size_t)xr + (size_t)xsr * 4; }
+  size_t bytes(int Bg) const { return (((size_t)Bg * per_row()) + 15) & ~(size_t)15; }
+};
 
 template <int MODE>
 static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xdt, int64_t ldx,
@@ -810,6 +878,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
                          int32_t* acc, int64_t M, int64_t K, int64_t B, hipStream_t st,
                          float xs_val = 0.f) {
   typedef ModeTraits<MODE> T;
+  typedef StageGeom<MODE> G;
   int rc = vqk_device_check();
   if (rc) return rc;
   if (!w || !ws || !out || (!x && !xq) || (xq && T::MX && !xsq)) return VQK_EINVAL;
@@ -824,10 +893,14 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   const int KB = (int)((MODE == M_MXFP4) ? K / 2 : K);
   const int cpr = KB / 128;
   const int depth = pick_depth(cpr);
-  const size_t lds_cap = 160 * 1024 - 1024;
+  const XLayout<MODE> xl = XLayout<MODE>::make(K);
+  const size_t lds_cap = 150 * 1024;
+  // The LDS-staged kernel needs whole 256-byte stages and 16-byte aligned scale rows; it
+  // reserves 4 waves x 2 stages of ring next to the activations.
+  const bool lds_path = VQK_LM_LDS && KB % 256 == 0 && ((uintptr_t)ws & 15) == 0;
+  const size_t ring2 = (size_t)4 * 2 * G::SLOT, ring4 = (size_t)4 * 4 * G::SLOT;
   // batch group size: up to 16*NCT rows, limited by LDS
-  const size_t per_row = (size_t)K * T::XB + (T::MX ? (size_t)K / 32 : 0);
-  int gmax = (int)((lds_cap - 64 - T::FB) / per_row);
+  int gmax = (int)(((lds_path ? lds_cap - ring2 : lds_cap) - 64) / xl.per_row());
   if (gmax < 1) return VQK_EUNSUPPORTED;
   const int nct_max = (MODE == M_W8A16) ? 1 : 2;
   if (gmax > 16 * nct_max) gmax = 16 * nct_max;
@@ -857,26 +930,28 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.Ball = (int)B;
     a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
     a.xs_val = xs_val;
-    const int NMF = (int)(K / T::KPM);
-    size_t lds = (size_t)NMF * 4 * Bg * T::FB + T::FB;
-    if (T::MX) lds += ((size_t)((NMF + 3) / 4) * 4 * Bg + 1) * 4;
-    lds = (lds + 15) & ~(size_t)15;
+    a.xr = xl.xr;
+    a.xsr = xl.xsr;
+    a.xs_off = Bg * xl.xr;
+    const size_t lds = xl.bytes(Bg);
     a.lds_x_bytes = (int)lds;
-    const int ntiles_l = (int)((M + 15) / 16);
-    const size_t lds_l = lds + (size_t)4 * VQK_LM_LDS_STAGES * LDS_STAGE;
-    if (VQK_LM_LDS && KB % 256 == 0 && lds_l <= 150 * 1024 && ((uintptr_t)ws & 15) == 0) {
-      int per_cu_l = (int)((150 * 1024) / (lds_l + 512));
+    const int ntiles = (int)((M + 15) / 16);
+    if (lds_path && lds + ring2 <= lds_cap) {
+      const int stages = (VQK_LM_LDS_STAGES >= 4 && lds + ring4 <= lds_cap) ? 4 : 2;
+      const size_t lds_l = lds + (stages == 4 ? ring4 : ring2);
+      int per_cu_l = (int)(lds_cap / (lds_l + 512));
       if (per_cu_l > VQK_LM_LDS_WG_PER_CU) per_cu_l = VQK_LM_LDS_WG_PER_CU;
       if (per_cu_l < 1) per_cu_l = 1;
       int grid_l = ncu * per_cu_l;
-      const int max_grid_l = (ntiles_l + 3) / 4;
+      const int max_grid_l = (ntiles + 3) / 4;
       if (grid_l > max_grid_l) grid_l = max_grid_l;
       const int nct_l = (Bg + 15) / 16;
       int rcl;
       if constexpr (MODE == M_W8A16) {
-        rcl = launch_lds<MODE, 1>(a, lds_l, grid_l, st);
+        rcl = launch_lds<MODE, 1>(a, stages, lds_l, grid_l, st);
       } else {
-        rcl = (nct_l == 1) ? launch_lds<MODE, 1>(a, lds_l, grid_l, st) : launch_lds<MODE, 2>(a, lds_l, grid_l, st);
+        rcl = (nct_l == 1) ? launch_lds<MODE, 1>(a, stages, lds_l, grid_l, st)
+                           : launch_lds<MODE, 2>(a, stages, lds_l, grid_l, st);
       }
       if (rcl) return rcl;
       continue;
@@ -884,7 +959,6 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     int per_cu = (int)((150 * 1024) / (lds + 1024));
     if (per_cu > VQK_LM_WG_PER_CU) per_cu = VQK_LM_WG_PER_CU;
     if (per_cu < 1) per_cu = 1;
-    const int ntiles = (int)((M + 15) / 16);
     int grid = ncu * per_cu;
     const int max_grid = (ntiles + (threads / 64) - 1) / (threads / 64);
     if (grid > max_grid) grid = max_grid;
