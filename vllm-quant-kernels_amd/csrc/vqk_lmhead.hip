@@ -54,6 +54,9 @@
 #ifndef VQK_LM_LDS_WG_PER_CU
 #define VQK_LM_LDS_WG_PER_CU 1
 #endif
+#ifndef VQK_LM_BALANCE
+#define VQK_LM_BALANCE 8   // batch groups up to this size: shrink the grid so every wave
+#endif                     // streams the same number of tiles
 #ifndef VQK_LM_NT_LDS
 #define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
 #endif
@@ -945,6 +948,12 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       int grid_l = ncu * per_cu_l;
       const int max_grid_l = (ntiles + 3) / 4;
       if (grid_l > max_grid_l) grid_l = max_grid_l;
+      if (Bg <= VQK_LM_BALANCE) {
+        // as few waves as still give every wave the same (maximal) number of tiles, so
+        // the stream keeps all of them busy to the end
+        const int tpw = (ntiles + 4 * grid_l - 1) / (4 * grid_l);
+        grid_l = ((ntiles + tpw - 1) / tpw + 3) / 4;
+      }
       const int nct_l = (Bg + 15) / 16;
       int rcl;
       if constexpr (MODE == M_W8A16) {
