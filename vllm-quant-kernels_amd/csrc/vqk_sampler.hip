@@ -13,18 +13,19 @@
 // scoring every element of a [32, 248320] batch is ALU-bound (~30 us).  The kernel prunes
 // exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
 // row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
-// A good L needs the whole row, so the work is two launches with no spinning or cross-
-// workgroup waits:
+// A good L needs the whole row, so the work is three launches with no spinning or
+// cross-workgroup waits:
 //   1. gumbel_cand_kernel streams the logits (256 threads x 64 floats per workgroup,
-//      coalesced 16-byte loads); greedy rows finish their argmax here; sampled rows score
-//      one candidate per thread (its largest raw logit) and publish the workgroup's best
+//      coalesced 16-byte loads); greedy rows take their argmax here; sampled rows score
+//      one candidate per thread (its largest raw logit); each workgroup publishes its best
 //      with one 64-bit atomicMax on (orderable(y) << 32 | ~v) - largest y, then smallest v;
-//   2. gumbel_surv_kernel re-reads only the sampled rows' slices (recently streamed, so
-//      mostly served by the 256 MB last-level cache), drops everything under the row's
-//      cutoff with one compare, scores the survivors through a per-wave LDS queue in full
-//      64-lane batches, and the last slice of each row writes the token and clears the
-//      row's workspace for the next call.
-// On the BASELINE logits about 13% of a B=32 batch survives.
+//   2. gumbel_surv_kernel re-reads the sampled rows (recently streamed, so mostly served by
+//      the 256 MB last-level cache) in small slices, drops everything under the row's
+//      cutoff with one compare and scores the survivors through a per-wave LDS queue in
+//      full 64-lane batches;
+//   3. gumbel_finish_kernel turns each row key into the token and clears it.
+// On the BASELINE logits about 19% of the sampled elements of a B=32 batch survive, almost
+// all of them in the rows with the highest temperatures.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,7 +52,6 @@ struct SmpArgs {
   const float* thr;
   int64_t* out;
   unsigned long long* keys;  // [B] row best key
-  unsigned int* done;        // [B] slices of the survivor launch finished
   int nchunks;
   int vec;                   // 16-byte loads allowed
   float* scores;             // debug: write y for every element (scores kernel only)
@@ -111,10 +111,8 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 // Cross-workgroup protocol.  Only device-scope atomics on the workspace are used, relaxed:
 // acquire/release fences would write back and invalidate the L2 of the issuing XCD
 // (buffer_wbl2 / buffer_inv), which costs far more than the whole reduction.  The ordering
-// that matters is enforced by waiting for an atomic to complete (s_waitcnt) before the next:
-// a slice's key max is performed before its done increment is issued, so the slice whose
-// increment returns nchunks-1 reads a key that holds every slice's max.  The launch boundary
-// orders launch 1's atomics before launch 2.
+// that matters is the one between launches, which the launch boundaries give: every atomic
+// of a launch is performed before the next launch reads the keys.
 __device__ __forceinline__ unsigned long long ld_relaxed_u64(unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -213,15 +211,20 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   if (tid == 0) amax_u64(&a.keys[row], gb);
 }
 
-// Launch 2.  Greedy rows: slice 0 writes the token.  Sampled rows: the row key holds every
-// slice's candidate, a value L the winner is >= to.  Since G <= GUMBEL_MAX for every Philox
-// word and rounding is monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is
-// one compare against a per-row raw-logit cutoff.  The slice's 64 floats per thread are
-// loaded at once; survivors are appended to a per-wave LDS queue (ballot + popcount) and
-// scored in full-wave batches of 128, two per lane (independent chains).  The last slice of
-// the row (per-row counter) writes the token and clears the row's workspace.
-constexpr int SURV_GROUP = 16;                     // elements appended between queue drains
-constexpr int QCAP = 128 + SURV_GROUP * 64;        // per-wave queue entries
+// Launch 2 (sampled rows only; greedy rows return at once).  The row key holds every
+// candidate, a score L the winner is >= to.  Since G <= GUMBEL_MAX for every Philox word
+// and rounding is monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is
+// one compare against a per-row raw-logit cutoff.  Survivors are appended to a per-wave
+// LDS queue (ballot + popcount) and scored in full-wave batches of 128, two per lane
+// (independent chains).  Survivors cluster in the rows with high temperature, so this pass
+// uses small slices (EPT elements per thread): many short workgroups let the dispatcher
+// spread one hot row over every CU.  A workgroup touches the row key only if it found a
+// better score than L, which is rare.
+template <int EPT>
+struct SurvCfg {
+  static constexpr int GROUP = EPT < 16 ? EPT : 16;  // elements appended between drains
+  static constexpr int QCAP = 128 + GROUP * 64;      // per-wave queue entries
+};
 
 __device__ __forceinline__ void drain128(const RowParams& p, float* qx, uint32_t* qv, int& qn, int lane,
                                          unsigned long long& best) {
@@ -236,25 +239,35 @@ __device__ __forceinline__ void drain128(const RowParams& p, float* qx, uint32_t
   }
 }
 
+template <int EPT>
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
+  typedef SurvCfg<EPT> C;
   __shared__ unsigned long long red[SMP_THREADS / 64];
-  __shared__ float qxs[SMP_THREADS / 64][QCAP];
-  __shared__ uint32_t qvs[SMP_THREADS / 64][QCAP];
+  __shared__ float qxs[SMP_THREADS / 64][C::QCAP];
+  __shared__ uint32_t qvs[SMP_THREADS / 64][C::QCAP];
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const RowParams p = row_params(a, row);
-  if (p.greedy) {
-    if (blockIdx.x == 0 && tid == 0) {
-      const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
-      a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
-      __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
+  if (p.greedy) return;
   const float* rowp = a.logits + (int64_t)row * a.ld;
-  const int base = blockIdx.x * SMP_CHUNK;
-  const bool full = a.vec && base + SMP_CHUNK <= a.V;
-  float xv[SMP_EPT];
-  load_slice(rowp, base, tid, a.V, full, xv);
+  const int base = blockIdx.x * (SMP_THREADS * EPT);
+  const bool full = a.vec && base + SMP_THREADS * EPT <= a.V;
+  float xv[EPT];
+  if (full) {
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) {
+      const v4f t = *(const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4);
+      xv[4 * i] = t.x;
+      xv[4 * i + 1] = t.y;
+      xv[4 * i + 2] = t.z;
+      xv[4 * i + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
+      xv[q] = rowp[v < a.V ? v : a.V - 1];
+    }
+  }
   const float NEG_INF = -__builtin_inff();
   const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
   const float L = from_orderable((uint32_t)(lk >> 32));
@@ -274,10 +287,10 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   unsigned long long best = 0ull;
   int qn = 0;
 #pragma unroll
-  for (int g0 = 0; g0 < SMP_EPT; g0 += SURV_GROUP) {
+  for (int g0 = 0; g0 < EPT; g0 += C::GROUP) {
 #pragma unroll
-    for (int q = g0; q < g0 + SURV_GROUP; ++q) {
-      const int v = slice_v(base, tid, q);
+    for (int q = g0; q < g0 + C::GROUP; ++q) {
+      const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
       const bool s = v < a.V && !(p.has_thr && !(xv[q] >= p.thr)) && !(xv[q] <= xc);
       const unsigned long long m = __ballot(s);
       const int pos = qn + __popcll(m & ((1ull << lane) - 1ull));
@@ -303,18 +316,16 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
     best = (k1 > best) ? k1 : best;
   }
   const unsigned long long gb = block_max_u64(best, red);
-  if (tid == 0) {
-    if (gb > lk) amax_u64(&a.keys[row], gb);
-    wait_vmem();
-    const unsigned int d = aadd_u32(&a.done[row], 1u);
-    if (d == (unsigned int)(a.nchunks - 1)) {
-      // every other slice's max was performed before its done increment returned
-      const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
-      a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
-      __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (tid == 0 && gb > lk) amax_u64(&a.keys[row], gb);
+}
+
+// Launch 3: the token of each row from its key, and the key cleared for the next call.
+__global__ void gumbel_finish_kernel(SmpArgs a) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= a.B) return;
+  const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
+  a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
+  __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Debug kernel: y for every element.
@@ -332,7 +343,7 @@ using namespace vqk;
 
 extern "C" int64_t vqk_gumbel_workspace_size(int64_t B) {
   if (B < 0) return 0;
-  return B * (int64_t)(sizeof(unsigned long long) + sizeof(unsigned int)) + 16;
+  return B * (int64_t)sizeof(unsigned long long) + 16;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
@@ -364,13 +375,19 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.thr = topk_thr;
   a.out = out;
   a.keys = (unsigned long long*)workspace;
-  a.done = (unsigned int*)((char*)workspace + B * sizeof(unsigned long long));
   a.nchunks = (int)((V + SMP_CHUNK - 1) / SMP_CHUNK);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                      (hipStream_t)stream, a);
-  hipLaunchKernelGGL(gumbel_surv_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
-                     (hipStream_t)stream, a);
+  // survivor pass: 1024 logits per workgroup for up to ~8M elements, else 4096
+  if (B * V <= ((int64_t)8 << 20)) {
+    const int ns = (int)((V + SMP_THREADS * 4 - 1) / (SMP_THREADS * 4));
+    hipLaunchKernelGGL(gumbel_surv_kernel<4>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+  } else {
+    const int ns = (int)((V + SMP_THREADS * 16 - 1) / (SMP_THREADS * 16));
+    hipLaunchKernelGGL(gumbel_surv_kernel<16>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+  }
+  hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }
