@@ -44,7 +44,7 @@ enum { VQK_F32 = 0, VQK_F16 = 1, VQK_BF16 = 2 };
 
 /* Library / device queries ---------------------------------------------------------- */
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change): 2. */
 int vqk_abi_version(void);
 
 /* Checks that the current HIP device is a gfx950 and records its CU count.
@@ -181,17 +181,17 @@ int vqk_gemm_mxfp4(const uint8_t *w_packed, const uint8_t *ws, const uint8_t *xq
  * G = -log(-log(max(u, 2^-126))), u = Philox4x32-10 word 0 of counter (v,0,0,0) and key
  * (seed lo32, seed hi32) mapped to [0,1) as Triton's uint_to_uniform_float does.
  * With topk_thr, y = -inf where x < thr[b] (raw logits).  out[b] = argmax_v y, smallest
- * index on ties.  One launch; the cross-block reduction happens inside it.
+ * index on ties.  Three launches on `stream` (candidates, survivors, finish); no host sync.
  *   logits   fp32 [B,V], row stride ld (elements), ld >= V.
  *   temp     fp32 [B] or NULL (NULL = plain argmax).
  *   seeds    int32 [B] (seed_is_64bit = 0; sign-extended to 64 bits) or int64 [B] (= 1).
  *   topk_thr fp32 [B] or NULL.
  *   out      int64 [B].
- *   workspace: >= vqk_gumbel_workspace_size(B) bytes of device memory that is all-zero
- *   before the FIRST launch that uses it; every launch leaves it all-zero again.
+ *   workspace: >= vqk_gumbel_workspace_size(B, V) bytes of device memory, 8-byte aligned,
+ *   all-zero before the FIRST launch that uses it; every launch leaves it all-zero again.
  * Replaces: fused_gumbel_sample + _gumbel_block_argmax_kernel
  *           (src/vllm_quant_kernels/_sampler_kernels.py:38-182). */
-int64_t vqk_gumbel_workspace_size(int64_t B);
+int64_t vqk_gumbel_workspace_size(int64_t B, int64_t V);
 int vqk_gumbel_argmax(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *temp, const void *seeds, int seed_is_64bit,
                       const float *topk_thr, int64_t *out, void *workspace,

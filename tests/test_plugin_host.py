@@ -294,7 +294,7 @@ def test_library_exports_header_symbols():
     missing = [d for d in decls if not hasattr(lib, d)]
     assert not missing, missing
     assert set(_lib.SIGNATURES) == decls, set(_lib.SIGNATURES) ^ decls
-    assert lib.vqk_abi_version() == 1
+    assert lib.vqk_abi_version() == 2
     assert _lib.strerror(-1) == "invalid argument" and _lib.strerror(-3) == "no gfx950 HIP device"
     nm = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
     exported = set(re.findall(r" T (vqk_[a-z0-9_]+)$", nm, re.M))

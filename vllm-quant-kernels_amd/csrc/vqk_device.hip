@@ -14,7 +14,7 @@ int g_cus[kMaxDev];
 std::mutex g_mu;
 }  // namespace
 
-extern "C" int vqk_abi_version(void) { return 1; }
+extern "C" int vqk_abi_version(void) { return 2; }
 
 extern "C" int vqk_device_check(void) {
   int dev = 0;

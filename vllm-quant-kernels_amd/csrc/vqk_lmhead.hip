@@ -129,7 +129,46 @@ struct LmArgs {
   int xr;               // LDS bytes per batch row of fragments (16 * odd)
   int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
   int xs_off;           // MX: LDS byte offset of the activation scales
+  int xvec;             // 1 when activation rows (x or xq) allow 16-byte loads
 };
+
+// N contiguous activation elements from element offset off as float (N % 8 == 0), with
+// 16-byte loads when the host found the rows aligned.  All loads are issued before any
+// conversion.
+template <int DT, int N>
+__device__ __forceinline__ void load_run(const void* x, int64_t off, bool vec, float (&out)[N]) {
+  if (vec) {
+    if constexpr (DT == VQK_F32) {
+      float4 t[N / 4];
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) t[i] = ((const float4*)((const float*)x + off))[i];
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        out[4 * i] = t[i].x;
+        out[4 * i + 1] = t[i].y;
+        out[4 * i + 2] = t[i].z;
+        out[4 * i + 3] = t[i].w;
+      }
+    } else {
+      uint4 t[N / 8];
+#pragma unroll
+      for (int i = 0; i < N / 8; ++i) t[i] = ((const uint4*)((const uint16_t*)x + off))[i];
+#pragma unroll
+      for (int i = 0; i < N / 8; ++i) {
+        const uint32_t w[4] = {t[i].x, t[i].y, t[i].z, t[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint16_t lo = (uint16_t)(w[j] & 0xFFFFu), hi = (uint16_t)(w[j] >> 16);
+          out[8 * i + 2 * j] = (DT == VQK_F16) ? h2f(lo) : bf2f(lo);
+          out[8 * i + 2 * j + 1] = (DT == VQK_F16) ? h2f(hi) : bf2f(hi);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = load_dt<DT>(x, off + e);
+  }
+}
 
 // ---------------------------------------------------------------------------------------
 // Prologue: stage the activations of this batch group into LDS in fragment order, one
@@ -151,9 +190,22 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
   if (MODE == M_W8A8 && !a.xq) {
     // per-tensor amax over the whole [Ball, K] activation (bit-exact max, order-free)
     float m = 0.f;
-    for (int b = 0; b < a.Ball; ++b) {
+    if (a.xvec) {
+      // 8 consecutive elements per step over the flattened [Ball, K/8] index space
+      const int per_row = K >> 3, total = a.Ball * per_row;
+#pragma unroll 4
+      for (int c = tid; c < total; c += nth) {
+        const int b = c / per_row, k8 = c - b * per_row;
+        float v[8];
+        load_run<DT, 8>(a.xall, (int64_t)b * a.ldx + 8 * k8, true, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+      }
+    } else {
+      for (int b = 0; b < a.Ball; ++b) {
 #pragma unroll 8
-      for (int k = tid; k < K; k += nth) m = fmaxf(m, fabsf(load_dt<DT>(a.xall, (int64_t)b * a.ldx + k)));
+        for (int k = tid; k < K; k += nth) m = fmaxf(m, fabsf(load_dt<DT>(a.xall, (int64_t)b * a.ldx + k)));
+      }
     }
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((tid & 63) == 0) lds_red[tid >> 6] = m;
@@ -180,18 +232,22 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
       uint32_t sbyte;
       if (a.xq) {
         const uint8_t* src = a.xq + (int64_t)b * K + 32 * grp;
+        if (a.xvec) {
+          const uint4 t0 = ((const uint4*)src)[0], t1 = ((const uint4*)src)[1];
+          v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
+          v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+        } else {
 #pragma unroll
-        for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+          for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+        }
         sbyte = a.xsq[(int64_t)b * G + grp];
       } else {
         const int64_t xo = (int64_t)b * a.ldx + 32 * grp;
         float xv[32];
+        load_run<DT, 32>(a.x, xo, a.xvec != 0, xv);
         float amax = 0.f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-          xv[e] = load_dt<DT>(a.x, xo + e);
-          amax = fmaxf(amax, fabsf(xv[e]));
-        }
+        for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(xv[e]));
         int kx = mx_exponent(amax, 448.0f);
         float sc = exp2i(kx);
 #pragma unroll
@@ -210,44 +266,101 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
       *sdst = (uint8_t)sbyte;
     }
   } else {
-    for (int f = tid; f < nfrag; f += nth) {
-      const int b = f % Bg;
-      const int gm = f / Bg;
-      const int g = gm & 3, mi = gm >> 2;
-      uint8_t* dst = lds + (size_t)b * a.xr + (size_t)gm * T::FB;
-      if (MODE == M_W8A16) {
-        const uint16_t* src = (const uint16_t*)a.x + (int64_t)b * a.ldx + frag_k<MODE>(mi, g, 0);
-        uint32_t v[4];
+    // U fragments per thread per round: every load of the round is issued before the
+    // first conversion, so a round costs one memory latency.
+    constexpr int U = (MODE == M_FP8) ? 1 : 4;
+    const bool vec = a.xvec != 0;
+    for (int f0 = tid; f0 < nfrag; f0 += U * nth) {
+      int fb[U], fgm[U];
+      bool ok[U];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
-        *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+      for (int u = 0; u < U; ++u) {
+        const int f = f0 + u * nth;
+        ok[u] = f < nfrag;
+        const int fc = ok[u] ? f : nfrag - 1;
+        fb[u] = fc % Bg;
+        fgm[u] = fc / Bg;
+      }
+      if constexpr (MODE == M_W8A16) {
+        // fp16 fragments are 8 consecutive halves of the row: copied as raw bits
+        uint4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int g = fgm[u] & 3, mi = fgm[u] >> 2;
+          const uint16_t* src = (const uint16_t*)a.x + (int64_t)fb[u] * a.ldx + frag_k<MODE>(mi, g, 0);
+          if (vec) {
+            raw[u] = *(const uint4*)src;
+          } else {
+            uint32_t v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+            raw[u] = make_uint4(v[0], v[1], v[2], v[3]);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (ok[u]) *(uint4*)(lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB) = raw[u];
+      } else if (a.xq) {
+        // pre-quantized bytes: element p of the fragment is row element frag_k(p), which
+        // comes in runs of 16 consecutive bytes
+        uint4 raw[U][T::FB / 16];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int g = fgm[u] & 3, mi = fgm[u] >> 2;
+#pragma unroll
+          for (int r = 0; r < T::FB / 16; ++r) {
+            const uint8_t* src = a.xq + (int64_t)fb[u] * K + frag_k<MODE>(mi, g, 16 * r);
+            if (vec) {
+              raw[u][r] = *(const uint4*)src;
+            } else {
+              uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+              for (int e = 0; e < 16; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+              raw[u][r] = make_uint4(v[0], v[1], v[2], v[3]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (!ok[u]) continue;
+          uint8_t* dst = lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB;
+#pragma unroll
+          for (int r = 0; r < T::FB / 16; ++r) *(uint4*)(dst + 16 * r) = raw[u][r];
+        }
       } else {
-        // W8A8 (16 bytes) or FP8 (32 bytes): element p of the fragment is row element frag_k(p)
-        // (the source test sits outside the element loops so their loads issue together)
-        uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if (a.xq) {
+        // W8A8 (16 elements) or FP8 (32 = two runs of 16): quantize from the exact float
+        float xv[U][T::FB];
 #pragma unroll
-          for (int p = 0; p < T::FB; ++p)
-            v[p >> 2] |= (uint32_t)a.xq[(int64_t)b * K + frag_k<MODE>(mi, g, p)] << (8 * (p & 3));
-        } else {
-          float xv[T::FB];
+        for (int u = 0; u < U; ++u) {
+          const int g = fgm[u] & 3, mi = fgm[u] >> 2;
 #pragma unroll
-          for (int p = 0; p < T::FB; ++p) xv[p] = load_dt<DT>(a.x, (int64_t)b * a.ldx + frag_k<MODE>(mi, g, p));
+          for (int r = 0; r < T::FB / 16; ++r) {
+            float run[16];
+            load_run<DT, 16>(a.x, (int64_t)fb[u] * a.ldx + frag_k<MODE>(mi, g, 16 * r), vec, run);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xv[u][16 * r + e] = run[e];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
           for (int p = 0; p < T::FB; ++p) {
             uint32_t byte;
             if (MODE == M_W8A8) {
-              float q = __builtin_rintf(xv[p] / xs_w8a8);
+              float q = __builtin_rintf(xv[u][p] / xs_w8a8);
               q = fminf(fmaxf(q, -127.f), 127.f);
               byte = (uint32_t)(uint8_t)(int8_t)(int)q;
             } else {
-              byte = f32_to_e4m3(xv[p]);
+              byte = f32_to_e4m3(xv[u][p]);
             }
             v[p >> 2] |= byte << (8 * (p & 3));
           }
+          if (!ok[u]) continue;
+          uint8_t* dst = lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB;
+          *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
+          if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
         }
-        *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-        if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
       }
     }
   }
@@ -934,6 +1047,12 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
     a.xs_val = xs_val;
     a.xr = xl.xr;
+    if (xq) {
+      a.xvec = ((uintptr_t)xq & 15) == 0 ? 1 : 0;  // rows are K bytes, K % 128 == 0
+    } else {
+      const int64_t es = (xdt == VQK_F32) ? 4 : 2;
+      a.xvec = (((uintptr_t)x & 15) == 0 && (ldx * es) % 16 == 0) ? 1 : 0;
+    }
     a.xsr = xl.xsr;
     a.xs_off = Bg * xl.xr;
     const size_t lds = xl.bytes(Bg);

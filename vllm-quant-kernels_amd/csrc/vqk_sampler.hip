@@ -21,8 +21,8 @@
 //      with one 64-bit atomicMax on (orderable(y) << 32 | ~v) - largest y, then smallest v;
 //   2. gumbel_surv_kernel re-reads the sampled rows (recently streamed, so mostly served by
 //      the 256 MB last-level cache) in small slices, drops everything under the row's
-//      cutoff with one compare and scores the survivors through a per-wave LDS queue in
-//      full 64-lane batches;
+//      cutoff with one compare and scores the survivors through a per-workgroup LDS
+//      queue, 64 per wave-step;
 //   3. gumbel_finish_kernel turns each row key into the token and clears it.
 // On the BASELINE logits about 19% of the sampled elements of a B=32 batch survive, almost
 // all of them in the rows with the highest temperatures.
@@ -52,6 +52,9 @@ struct SmpArgs {
   const float* thr;
   int64_t* out;
   unsigned long long* keys;  // [B] row best key
+  uint32_t* bkeys;           // [B, nblk] orderable key of each 1024-logit block's largest
+                             // admissible logit (0: none)
+  int nblk;
   int nchunks;
   int vec;                   // 16-byte loads allowed
   float* scores;             // debug: write y for every element (scores kernel only)
@@ -182,7 +185,8 @@ __device__ __forceinline__ void load_slice(const float* rowp, int base, int tid,
 // to the row with one fire-and-forget 64-bit atomicMax.
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   __shared__ unsigned long long red[SMP_THREADS / 64];
-  const int row = blockIdx.y, tid = threadIdx.x;
+  __shared__ uint32_t bred[SMP_THREADS / 64][16];
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const int base = blockIdx.x * SMP_CHUNK;
   const bool full = a.vec && base + SMP_CHUNK <= a.V;
@@ -190,15 +194,53 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   load_slice(rowp, base, tid, a.V, full, xv);
   const RowParams p = row_params(a, row);
   const float NEG_INF = -__builtin_inff();
-  uint32_t km = 0u;  // below orderable(-inf)
+  const float thr = p.has_thr ? p.thr : NEG_INF;  // x < thr is masked (NaN is not)
+  // One pass: the thread's best key (greedy: y itself; sampled: the raw logit, which ranks
+  // the candidates) and the best key of each of its 16 element groups (group i of every
+  // thread is 1024-logit block i of the slice).  Inadmissible elements count as -inf, out
+  // of range ones as key 0, below every real key.
+  uint32_t km = 0u;
   int qm = -1;
+  uint32_t mb[16];
+  bool slow = !full;
+  if (full) {
+    // Fast form in float compares: strict > keeps the first index and treats -0 == +0;
+    // NaN (which must rank above everything) only raises a flag that sends the thread to
+    // the key form below.
+    float m = NEG_INF, mf[16];
+    int qf = 0;
+    bool nan = false;
 #pragma unroll
-  for (int q = 0; q < SMP_EPT; ++q) {
-    const bool in = slice_v(base, tid, q) < a.V;
-    const bool adm = !(p.has_thr && !(xv[q] >= p.thr));
-    // greedy: y itself; sampled: the raw logit ranks the candidates (inadmissible as -inf)
-    const uint32_t k = in ? orderable(adm ? xv[q] : NEG_INF) : 0u;
-    take_max(k, q, km, qm);
+    for (int i = 0; i < 16; ++i) mf[i] = NEG_INF;
+#pragma unroll
+    for (int q = 0; q < SMP_EPT; ++q) {
+      const float x = xv[q] < thr ? NEG_INF : xv[q];
+      nan = nan || (x != x);
+      const bool b = x > m;
+      m = b ? x : m;
+      qf = b ? q : qf;
+      mf[q >> 2] = fmaxf(mf[q >> 2], x);
+    }
+    if (!nan) {
+      km = orderable(m);
+      qm = qf;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mb[i] = orderable(mf[i]);
+    }
+    slow = nan;
+  }
+  if (slow) {
+    // Key form: orderable keys (NaN on top); out-of-range elements are key 0.
+    km = 0u;
+    qm = -1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mb[i] = 0u;
+#pragma unroll
+    for (int q = 0; q < SMP_EPT; ++q) {
+      const uint32_t k = slice_v(base, tid, q) < a.V ? orderable(xv[q] < thr ? NEG_INF : xv[q]) : 0u;
+      take_max(k, q, km, qm);
+      mb[q >> 2] = k > mb[q >> 2] ? k : mb[q >> 2];
+    }
   }
   unsigned long long best = 0ull;
   if (qm >= 0) {
@@ -207,6 +249,36 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
     if (!p.greedy && y > NEG_INF) y = score(p, y, v);
     best = make_key(y, v);
   }
+  if (!p.greedy) {
+    // Block maxima for the survivor pass.  A butterfly that halves the values at each of
+    // its first four steps leaves lane l with the wave's maximum of block (l >> 2) & 15.
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+      const int half = 8 >> step, bit = 32 >> step;
+      const bool up = (lane & bit) != 0;
+#pragma unroll
+      for (int j = 0; j < half; ++j) {
+        const uint32_t send = up ? mb[j] : mb[j + half];
+        const uint32_t keep = up ? mb[j + half] : mb[j];
+        const uint32_t got = (uint32_t)__shfl_xor((int)send, bit);
+        mb[j] = got > keep ? got : keep;
+      }
+    }
+#pragma unroll
+    for (int bit = 2; bit >= 1; bit >>= 1) {
+      const uint32_t got = (uint32_t)__shfl_xor((int)mb[0], bit);
+      mb[0] = got > mb[0] ? got : mb[0];
+    }
+    if ((lane & 3) == 0) bred[tid >> 6][lane >> 2] = mb[0];
+    __syncthreads();
+    const int blk = blockIdx.x * 16 + tid;
+    if (tid < 16 && blk < a.nblk) {
+      uint32_t k = bred[0][tid];
+#pragma unroll
+      for (int w = 1; w < SMP_THREADS / 64; ++w) k = bred[w][tid] > k ? bred[w][tid] : k;
+      a.bkeys[(int64_t)row * a.nblk + blk] = k;
+    }
+  }
   const unsigned long long gb = block_max_u64(best, red);
   if (tid == 0) amax_u64(&a.keys[row], gb);
 }
@@ -214,40 +286,51 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
 // Launch 2 (sampled rows only; greedy rows return at once).  The row key holds every
 // candidate, a score L the winner is >= to.  Since G <= GUMBEL_MAX for every Philox word
 // and rounding is monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is
-// one compare against a per-row raw-logit cutoff.  Survivors are appended to a per-wave
-// LDS queue (ballot + popcount) and scored in full-wave batches of 128, two per lane
-// (independent chains).  Survivors cluster in the rows with high temperature, so this pass
-// uses small slices (EPT elements per thread): many short workgroups let the dispatcher
-// spread one hot row over every CU.  A workgroup touches the row key only if it found a
-// better score than L, which is rare.
-template <int EPT>
-struct SurvCfg {
-  static constexpr int GROUP = EPT < 16 ? EPT : 16;  // elements appended between drains
-  static constexpr int QCAP = 128 + GROUP * 64;      // per-wave queue entries
-};
-
-__device__ __forceinline__ void drain128(const RowParams& p, float* qx, uint32_t* qv, int& qn, int lane,
-                                         unsigned long long& best) {
-  while (qn >= 128) {
-    qn -= 128;
-    const float x0 = qx[qn + lane], x1 = qx[qn + 64 + lane];
-    const uint32_t v0 = qv[qn + lane], v1 = qv[qn + 64 + lane];
-    const unsigned long long k0 = make_key(score(p, x0, v0), v0);
-    const unsigned long long k1 = make_key(score(p, x1, v1), v1);
-    best = (k0 > best) ? k0 : best;
-    best = (k1 > best) ? k1 : best;
-  }
-}
+// one compare against a per-row raw-logit cutoff; whole 1024-logit blocks whose largest
+// admissible logit is under the cutoff are skipped unread.  Survivors cluster in the rows
+// with high temperature, so this pass uses small slices (EPT elements per thread): many
+// short workgroups let the dispatcher spread one hot row over every CU.  A workgroup
+// touches the row key only if it found a better score than L, which is rare.
 
 template <int EPT>
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
-  typedef SurvCfg<EPT> C;
+  constexpr int CAP = SMP_THREADS * EPT;  // every element of the slice may survive
   __shared__ unsigned long long red[SMP_THREADS / 64];
-  __shared__ float qxs[SMP_THREADS / 64][C::QCAP];
-  __shared__ uint32_t qvs[SMP_THREADS / 64][C::QCAP];
-  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float qx[CAP];
+  __shared__ uint32_t qv[CAP];
+  __shared__ int qn;
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const RowParams p = row_params(a, row);
   if (p.greedy) return;
+  const float NEG_INF = -__builtin_inff();
+  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
+  const float L = from_orderable((uint32_t)(lk >> 32));
+  float xc = NEG_INF;
+  if (L > NEG_INF && L == L) {
+    float c = (L - GUMBEL_MAX) * p.T;
+    for (int it = 0; it < 16; ++it) {
+      if ((c / p.T) + GUMBEL_MAX < L) {
+        xc = c;
+        break;
+      }
+      c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
+    }
+  }
+  // skip the slice without reading it when no block of it has an admissible logit > xc
+  // (wave-uniform: every thread reads the same keys)
+  {
+    constexpr int NB = EPT / 4;  // 1024-logit blocks per slice
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int blk = blockIdx.x * NB + i;
+      if (blk < a.nblk) {
+        const uint32_t k = a.bkeys[(int64_t)row * a.nblk + blk];
+        any = any || (k != 0u && !(from_orderable(k) <= xc));
+      }
+    }
+    if (!any) return;
+  }
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const int base = blockIdx.x * (SMP_THREADS * EPT);
   const bool full = a.vec && base + SMP_THREADS * EPT <= a.V;
@@ -268,64 +351,51 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
       xv[q] = rowp[v < a.V ? v : a.V - 1];
     }
   }
-  const float NEG_INF = -__builtin_inff();
-  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
-  const float L = from_orderable((uint32_t)(lk >> 32));
-  float xc = NEG_INF;
-  if (L > NEG_INF && L == L) {
-    float c = (L - GUMBEL_MAX) * p.T;
-    for (int it = 0; it < 16; ++it) {
-      if ((c / p.T) + GUMBEL_MAX < L) {
-        xc = c;
-        break;
-      }
-      c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
-    }
-  }
-  float* qx = qxs[wave];
-  uint32_t* qv = qvs[wave];
-  unsigned long long best = 0ull;
-  int qn = 0;
+  // Survivors of the whole workgroup go to one LDS queue (one LDS atomic per wave and
+  // element step reserves the wave's run), then every thread scores queue entries tid,
+  // tid + 256, ...: n survivors cost ceil(n / 64) wave-scores however they are spread.
+  if (tid == 0) qn = 0;
+  __syncthreads();
 #pragma unroll
-  for (int g0 = 0; g0 < EPT; g0 += C::GROUP) {
-#pragma unroll
-    for (int q = g0; q < g0 + C::GROUP; ++q) {
-      const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
-      const bool s = v < a.V && !(p.has_thr && !(xv[q] >= p.thr)) && !(xv[q] <= xc);
-      const unsigned long long m = __ballot(s);
-      const int pos = qn + __popcll(m & ((1ull << lane) - 1ull));
+  for (int q = 0; q < EPT; ++q) {
+    const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
+    const bool s = v < a.V && !(p.has_thr && !(xv[q] >= p.thr)) && !(xv[q] <= xc);
+    const unsigned long long m = __ballot(s);
+    if (m) {
+      int wbase = 0;
+      if (lane == 0)
+        wbase = __hip_atomic_fetch_add(&qn, (int)__popcll(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      wbase = __shfl(wbase, 0);
       if (s) {
+        const int pos = wbase + (int)__popcll(m & ((1ull << lane) - 1ull));
         qx[pos] = xv[q];
         qv[pos] = (uint32_t)v;
       }
-      qn += __popcll(m);
     }
-    __builtin_amdgcn_wave_barrier();
-    drain128(p, qx, qv, qn, lane, best);
-    __builtin_amdgcn_wave_barrier();
   }
-  if (lane < qn) {
-    const float x0 = qx[lane];
-    const uint32_t v0 = qv[lane];
-    const bool has1 = lane + 64 < qn;
-    const float x1 = has1 ? qx[lane + 64] : x0;
-    const uint32_t v1 = has1 ? qv[lane + 64] : v0;
-    const unsigned long long k0 = make_key(score(p, x0, v0), v0);
-    const unsigned long long k1 = make_key(score(p, x1, v1), v1);
-    best = (k0 > best) ? k0 : best;
-    best = (k1 > best) ? k1 : best;
+  __syncthreads();
+  const int n = qn;
+  unsigned long long best = 0ull;
+  for (int i = tid; i < n; i += SMP_THREADS) {
+    const float x = qx[i];
+    const uint32_t v = qv[i];
+    const unsigned long long k = make_key(score(p, x, v), v);
+    best = (k > best) ? k : best;
   }
   const unsigned long long gb = block_max_u64(best, red);
   if (tid == 0 && gb > lk) amax_u64(&a.keys[row], gb);
 }
 
-// Launch 3: the token of each row from its key, and the key cleared for the next call.
+// Launch 3: the token of each row from its key; the whole workspace (keys and block keys)
+// is cleared for the next call, whatever its batch size.
 __global__ void gumbel_finish_kernel(SmpArgs a) {
-  const int row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= a.B) return;
-  const unsigned long long k = ld_relaxed_u64(&a.keys[row]);
-  a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
-  __hip_atomic_store(&a.keys[row], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < a.B) {
+    const unsigned long long k = ld_relaxed_u64(&a.keys[i]);
+    a.out[i] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
+    __hip_atomic_store(&a.keys[i], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (i < a.B * a.nblk) a.bkeys[i] = 0u;
 }
 
 // Debug kernel: y for every element.
@@ -341,9 +411,11 @@ __global__ void gumbel_scores_kernel(SmpArgs a) {
 
 using namespace vqk;
 
-extern "C" int64_t vqk_gumbel_workspace_size(int64_t B) {
-  if (B < 0) return 0;
-  return B * (int64_t)sizeof(unsigned long long) + 16;
+static int64_t gumbel_nblk(int64_t V) { return (V + 1023) / 1024; }
+
+extern "C" int64_t vqk_gumbel_workspace_size(int64_t B, int64_t V) {
+  if (B < 0 || V < 0) return 0;
+  return B * (int64_t)sizeof(unsigned long long) + B * gumbel_nblk(V) * (int64_t)sizeof(uint32_t) + 16;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
@@ -362,7 +434,7 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   if (rc) return rc;
   if (!out || !workspace) return VQK_EINVAL;
   if (B == 0) return VQK_OK;
-  if (ws_bytes < vqk_gumbel_workspace_size(B)) return VQK_EWORKSPACE;
+  if (ws_bytes < vqk_gumbel_workspace_size(B, V)) return VQK_EWORKSPACE;
   if (((uintptr_t)workspace & 7) != 0) return VQK_EINVAL;
   SmpArgs a = {};
   a.logits = logits;
@@ -375,6 +447,8 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.thr = topk_thr;
   a.out = out;
   a.keys = (unsigned long long*)workspace;
+  a.bkeys = (uint32_t*)((char*)workspace + B * sizeof(unsigned long long));
+  a.nblk = (int)gumbel_nblk(V);
   a.nchunks = (int)((V + SMP_CHUNK - 1) / SMP_CHUNK);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
@@ -387,7 +461,8 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
     const int ns = (int)((V + SMP_THREADS * 16 - 1) / (SMP_THREADS * 16));
     hipLaunchKernelGGL(gumbel_surv_kernel<16>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
-  hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
+  const int64_t nfin = B * (int64_t)a.nblk;
+  hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((nfin + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }

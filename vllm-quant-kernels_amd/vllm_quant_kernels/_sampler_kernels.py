@@ -1,4 +1,4 @@
-"""Fused Gumbel-argmax sampling over [B, V] fp32 logits, one HIP launch.
+"""Fused Gumbel-argmax sampling over [B, V] fp32 logits (three short HIP launches).
 
 Replaces the reference's Triton block-argmax kernel plus its two-op host tail
 (src/vllm_quant_kernels/_sampler_kernels.py:38-182) with ``vqk_gumbel_argmax``: the
@@ -26,11 +26,11 @@ _ws_lock = threading.Lock()
 _workspaces: dict = {}
 
 
-def _workspace(device: torch.device, stream: int, B: int) -> torch.Tensor:
+def _workspace(device: torch.device, stream: int, B: int, V: int) -> torch.Tensor:
     """Per (device, stream) zero-initialised workspace; the kernel leaves it zeroed again,
     so it is cleared only when first created or grown.  Launches on one stream are ordered,
     so sharing it among them is safe; different streams get different workspaces."""
-    need = int(_lib.load().vqk_gumbel_workspace_size(B))
+    need = int(_lib.load().vqk_gumbel_workspace_size(B, V))
     key = (device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
@@ -71,7 +71,7 @@ def fused_gumbel_sample(
     if B == 0:
         return out
     stream = torch.cuda.current_stream(logits.device).cuda_stream
-    ws = _workspace(logits.device, stream, B)
+    ws = _workspace(logits.device, stream, B, V)
     _lib.call(
         "vqk_gumbel_argmax",
         logits.data_ptr(), logits.stride(0), B, V,
