@@ -960,6 +960,8 @@ static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, h
   // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
   if (stages == 4)
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4>), dim3(grid), dim3(256), lds_bytes, st, a);
+  else if (stages == 3)
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 3>), dim3(grid), dim3(256), lds_bytes, st, a);
   else
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 2>), dim3(grid), dim3(256), lds_bytes, st, a);
   hipError_t e = hipGetLastError();
@@ -1059,8 +1061,11 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.lds_x_bytes = (int)lds;
     const int ntiles = (int)((M + 15) / 16);
     if (lds_path && lds + ring2 <= lds_cap) {
-      const int stages = (VQK_LM_LDS_STAGES >= 4 && lds + ring4 <= lds_cap) ? 4 : 2;
-      const size_t lds_l = lds + (stages == 4 ? ring4 : ring2);
+      // the deepest ring (4, 3 or 2 stages per wave) that fits next to the activations
+      const size_t ring3 = (size_t)4 * 3 * G::SLOT;
+      const int stages = (VQK_LM_LDS_STAGES >= 4 && lds + ring4 <= lds_cap) ? 4
+                         : (VQK_LM_LDS_STAGES >= 3 && lds + ring3 <= lds_cap) ? 3 : 2;
+      const size_t lds_l = lds + (size_t)4 * stages * G::SLOT;
       int per_cu_l = (int)(lds_cap / (lds_l + 512));
       if (per_cu_l > VQK_LM_LDS_WG_PER_CU) per_cu_l = VQK_LM_LDS_WG_PER_CU;
       if (per_cu_l < 1) per_cu_l = 1;

@@ -300,10 +300,19 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   __shared__ uint32_t qv[CAP];
   __shared__ int qn;
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  // every per-row and per-block value this workgroup needs is loaded at once, so the
+  // decision to skip costs one memory latency
+  constexpr int NB = EPT / 4;  // 1024-logit blocks per slice
+  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
+  uint32_t bk[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int blk = blockIdx.x * NB + i;
+    bk[i] = blk < a.nblk ? a.bkeys[(int64_t)row * a.nblk + blk] : 0u;
+  }
   const RowParams p = row_params(a, row);
   if (p.greedy) return;
   const float NEG_INF = -__builtin_inff();
-  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
   const float L = from_orderable((uint32_t)(lk >> 32));
   float xc = NEG_INF;
   if (L > NEG_INF && L == L) {
@@ -319,16 +328,9 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   // skip the slice without reading it when no block of it has an admissible logit > xc
   // (wave-uniform: every thread reads the same keys)
   {
-    constexpr int NB = EPT / 4;  // 1024-logit blocks per slice
     bool any = false;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int blk = blockIdx.x * NB + i;
-      if (blk < a.nblk) {
-        const uint32_t k = a.bkeys[(int64_t)row * a.nblk + blk];
-        any = any || (k != 0u && !(from_orderable(k) <= xc));
-      }
-    }
+    for (int i = 0; i < NB; ++i) any = any || (bk[i] != 0u && !(from_orderable(bk[i]) <= xc));
     if (!any) return;
   }
   const float* rowp = a.logits + (int64_t)row * a.ld;
