@@ -57,6 +57,11 @@
 #ifndef VQK_LM_BALANCE
 #define VQK_LM_BALANCE 8   // batch groups up to this size: shrink the grid so every wave
 #endif                     // streams the same number of tiles
+#ifndef VQK_LM_SC_POLICY
+// cache policy of the MX scale pieces (a stage reads 8-16 bytes of each row's scale line and
+// the following stages read the rest of that line)
+#define VQK_LM_SC_POLICY 2
+#endif
 #ifndef VQK_LM_NT_LDS
 #define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
 #endif
@@ -132,43 +137,6 @@ struct LmArgs {
   int xvec;             // 1 when activation rows (x or xq) allow 16-byte loads
 };
 
-// N contiguous activation elements from element offset off as float (N % 8 == 0), with
-// 16-byte loads when the host found the rows aligned.  All loads are issued before any
-// conversion.
-template <int DT, int N>
-__device__ __forceinline__ void load_run(const void* x, int64_t off, bool vec, float (&out)[N]) {
-  if (vec) {
-    if constexpr (DT == VQK_F32) {
-      float4 t[N / 4];
-#pragma unroll
-      for (int i = 0; i < N / 4; ++i) t[i] = ((const float4*)((const float*)x + off))[i];
-#pragma unroll
-      for (int i = 0; i < N / 4; ++i) {
-        out[4 * i] = t[i].x;
-        out[4 * i + 1] = t[i].y;
-        out[4 * i + 2] = t[i].z;
-        out[4 * i + 3] = t[i].w;
-      }
-    } else {
-      uint4 t[N / 8];
-#pragma unroll
-      for (int i = 0; i < N / 8; ++i) t[i] = ((const uint4*)((const uint16_t*)x + off))[i];
-#pragma unroll
-      for (int i = 0; i < N / 8; ++i) {
-        const uint32_t w[4] = {t[i].x, t[i].y, t[i].z, t[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint16_t lo = (uint16_t)(w[j] & 0xFFFFu), hi = (uint16_t)(w[j] >> 16);
-          out[8 * i + 2 * j] = (DT == VQK_F16) ? h2f(lo) : bf2f(lo);
-          out[8 * i + 2 * j + 1] = (DT == VQK_F16) ? h2f(hi) : bf2f(hi);
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < N; ++e) out[e] = load_dt<DT>(x, off + e);
-  }
-}
 
 // ---------------------------------------------------------------------------------------
 // Prologue: stage the activations of this batch group into LDS in fragment order, one
@@ -220,6 +188,7 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
   } else if (MODE == M_W8A8) {
     if (tid == 0) lds_red[16] = xs_w8a8;
   }
+  const float xs_inv = 1.0f / xs_w8a8;  // W8A8: reciprocal for rint_div_i8 (IEEE division)
 
   if constexpr (T::MX) {
     // one 32-element MX group per work item; its 32 bytes land in two 16-byte halves of the
@@ -348,7 +317,7 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
           for (int p = 0; p < T::FB; ++p) {
             uint32_t byte;
             if (MODE == M_W8A8) {
-              float q = __builtin_rintf(xv[u][p] / xs_w8a8);
+              float q = rint_div_i8(xv[u][p], xs_w8a8, xs_inv);
               q = fminf(fmaxf(q, -127.f), 127.f);
               byte = (uint32_t)(uint8_t)(int8_t)(int)q;
             } else {
@@ -793,10 +762,10 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
     const uint8_t* sb = (const uint8_t*)a.ws + (int64_t)t * 16 * (a.K >> 5) + G::SB * ks;
     if (MODE == M_MXFP8) {
       if (lane < 32)
-        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 4, 0, VQK_LM_NT_LDS);
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 4, 0, VQK_LM_SC_POLICY);
     } else {
       if (lane < 16)
-        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 16, 0, VQK_LM_NT_LDS);
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 16, 0, VQK_LM_SC_POLICY);
     }
   }
 }

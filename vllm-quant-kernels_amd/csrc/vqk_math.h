@@ -47,6 +47,56 @@ __device__ __forceinline__ float load_dt(const void* p, int64_t i) {
   else return bf2f(((const uint16_t*)p)[i]);
 }
 
+// N contiguous elements (dtype code DT) from element offset off as float (N % 8 == 0), with
+// 16-byte loads when the host found the rows aligned.  All loads are issued before any
+// conversion.
+template <int DT, int N>
+__device__ __forceinline__ void load_run(const void* x, int64_t off, bool vec, float (&out)[N]) {
+  if (vec) {
+    if constexpr (DT == VQK_F32) {
+      float4 t[N / 4];
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) t[i] = ((const float4*)((const float*)x + off))[i];
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        out[4 * i] = t[i].x;
+        out[4 * i + 1] = t[i].y;
+        out[4 * i + 2] = t[i].z;
+        out[4 * i + 3] = t[i].w;
+      }
+    } else {
+      uint4 t[N / 8];
+#pragma unroll
+      for (int i = 0; i < N / 8; ++i) t[i] = ((const uint4*)((const uint16_t*)x + off))[i];
+#pragma unroll
+      for (int i = 0; i < N / 8; ++i) {
+        const uint32_t w[4] = {t[i].x, t[i].y, t[i].z, t[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint16_t lo = (uint16_t)(w[j] & 0xFFFFu), hi = (uint16_t)(w[j] >> 16);
+          out[8 * i + 2 * j] = (DT == VQK_F16) ? h2f(lo) : bf2f(lo);
+          out[8 * i + 2 * j + 1] = (DT == VQK_F16) ? h2f(hi) : bf2f(hi);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = load_dt<DT>(x, off + e);
+  }
+}
+
+// rint(fl(x / s)) for |x / s| <= 128 (int8 quantization) with one multiply in the common
+// case.  r = fl(1/s); t = x*r differs from x/s by at most 2^-23 * 128 = 2^-16, and fl(x/s)
+// from x/s by at most 2^-17, so t and fl(x/s) are within 2^-15 of each other: unless a
+// half-integer lies that close to t, both round to the same integer.  Otherwise (rare) the
+// IEEE division decides, ties included.
+__device__ __forceinline__ float rint_div_i8(float x, float s, float r) {
+  float t = x * r;
+  const float h = floorf(t) + 0.5f;
+  if (fabsf(t - h) < 3.0517578125e-05f) t = x / s;  // 2^-15
+  return __builtin_rintf(t);
+}
+
 // ---------------------------------------------------------------------------------------
 // OCP float8_e4m3fn encoding with torch's cast semantics (Appendix of the plugin notes):
 // round to nearest even; no saturation: anything that rounds above 448 is NaN (0x7F),

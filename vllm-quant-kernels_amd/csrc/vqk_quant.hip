@@ -68,21 +68,21 @@ __global__ void __launch_bounds__(QT) quant_rows_fp8_kernel(const void* w, int d
   if (threadIdx.x == 0) sout[row] = f2h(s);
 }
 
-// One thread per 32-element group.
-__global__ void quant_mx_kernel(const void* t, int dt, int64_t R, int64_t K, int64_t ldt, uint8_t* q,
-                                uint8_t* scales, int fp4) {
+// One thread per 32-element group; the group's 32 elements come in with 16-byte loads when
+// rows are 16-byte aligned (vec).
+template <int DT>
+__global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt, uint8_t* q,
+                                uint8_t* scales, int fp4, int vec) {
   const int64_t G = K / 32;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= R * G) return;
   const int64_t row = gid / G, grp = gid - row * G;
   const int64_t off = row * ldt + grp * 32;
   float v[32];
+  load_run<DT, 32>(t, off, vec != 0, v);
   float amax = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    v[e] = load_as_f32(t, dt, off + e);
-    amax = fmaxf(amax, fabsf(v[e]));
-  }
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
   const int k = mx_exponent(amax, fp4 ? 6.0f : 448.0f);
   const float sc = exp2i(k);
   scales[row * G + grp] = (uint8_t)(k + 127);
@@ -177,7 +177,14 @@ static int quant_mx(const void* t, int dt, int64_t R, int64_t K, int64_t ldt, ui
   const int th = 256;
   const int64_t nb = (n + th - 1) / th;
   if (nb > INT32_MAX) return VQK_EUNSUPPORTED;
-  hipLaunchKernelGGL(quant_mx_kernel, dim3((unsigned)nb), dim3(th), 0, st, t, dt, R, K, ldt, q, s, fp4);
+  const int es = (dt == VQK_F32) ? 4 : 2;
+  const int vec = (((uintptr_t)t & 15) == 0 && (ldt * es) % 16 == 0) ? 1 : 0;
+  if (dt == VQK_F32)
+    hipLaunchKernelGGL(quant_mx_kernel<VQK_F32>, dim3((unsigned)nb), dim3(th), 0, st, t, R, K, ldt, q, s, fp4, vec);
+  else if (dt == VQK_F16)
+    hipLaunchKernelGGL(quant_mx_kernel<VQK_F16>, dim3((unsigned)nb), dim3(th), 0, st, t, R, K, ldt, q, s, fp4, vec);
+  else
+    hipLaunchKernelGGL(quant_mx_kernel<VQK_BF16>, dim3((unsigned)nb), dim3(th), 0, st, t, R, K, ldt, q, s, fp4, vec);
   return finish();
 }
 

@@ -456,12 +456,14 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                      (hipStream_t)stream, a);
   // survivor pass: 1024 logits per workgroup for up to ~8M elements, else 4096
-  if (B * V <= ((int64_t)8 << 20)) {
+  // survivor slices: 1024 logits per workgroup for small batches (more workgroups to spread
+  // a hot row over), 2048 beyond ~2M elements (measured best at B = 32 and 128)
+  if (B * V <= ((int64_t)2 << 20)) {
     const int ns = (int)((V + SMP_THREADS * 4 - 1) / (SMP_THREADS * 4));
     hipLaunchKernelGGL(gumbel_surv_kernel<4>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   } else {
-    const int ns = (int)((V + SMP_THREADS * 16 - 1) / (SMP_THREADS * 16));
-    hipLaunchKernelGGL(gumbel_surv_kernel<16>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+    const int ns = (int)((V + SMP_THREADS * 8 - 1) / (SMP_THREADS * 8));
+    hipLaunchKernelGGL(gumbel_surv_kernel<8>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
   const int64_t nfin = B * (int64_t)a.nblk;
   hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((nfin + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
