@@ -187,8 +187,8 @@ int vqk_gemm_mxfp4(const uint8_t *w_packed, const uint8_t *ws, const uint8_t *xq
  *   seeds    int32 [B] (seed_is_64bit = 0; sign-extended to 64 bits) or int64 [B] (= 1).
  *   topk_thr fp32 [B] or NULL.
  *   out      int64 [B].
- *   workspace: >= vqk_gumbel_workspace_size(B, V) bytes of device memory, 8-byte aligned,
- *   all-zero before the FIRST launch that uses it; every launch leaves it all-zero again.
+ *   workspace: >= vqk_gumbel_workspace_size(B, V) bytes of device memory, 8-byte aligned;
+ *   no initialisation needed (every launch writes each value before reading it).
  * Replaces: fused_gumbel_sample + _gumbel_block_argmax_kernel
  *           (src/vllm_quant_kernels/_sampler_kernels.py:38-182). */
 int64_t vqk_gumbel_workspace_size(int64_t B, int64_t V);

@@ -1,7 +1,7 @@
 """HIP-graph capture of the hot path: every replay must equal the eager result.
 
-The lm_head and sampler launches allocate nothing and issue no memset (the sampler's
-workspace is cleared by its own last workgroup), so both are capturable.  As a guard
+The lm_head and sampler launches allocate nothing and issue no memset (every sampler
+launch writes each workspace value before reading it), so both are capturable.  As a guard
 against replay-dependent state, each graph is replayed several times with unrelated eager
 work and synchronizations in between, and every replay is compared with eager execution.
 """

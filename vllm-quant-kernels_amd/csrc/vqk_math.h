@@ -172,14 +172,38 @@ __device__ __forceinline__ float exp2i(int k) {
 constexpr uint32_t PHILOX_MA = 0xD2511F53u, PHILOX_MB = 0xCD9E8D57u;
 constexpr uint32_t PHILOX_WA = 0x9E3779B9u, PHILOX_WB = 0xBB67AE85u;
 
+// a ^ b ^ k as one v_bitop3_b32 (truth table 0x96: odd parity); k must be wave-uniform.
+__device__ __forceinline__ uint32_t xor3_vvs(uint32_t a, uint32_t b, uint32_t k) {
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+}
+
+// The key (k0, k1) must be wave-uniform (every caller keys a whole row with one seed).
 __device__ __forceinline__ uint32_t philox_word0(uint32_t v, uint32_t k0, uint32_t k1) {
   uint32_t c0 = v, c1 = 0u, c2 = 0u, c3 = 0u;
+  // Rounds 0 and 1 in plain C, which the compiler folds: c1 = c2 = c3 = 0 at first, and
+  // word 0 after round 0 is the key itself, so round 1's Ma product is uniform.
 #pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    uint64_t pa = (uint64_t)PHILOX_MA * c0;
-    uint64_t pb = (uint64_t)PHILOX_MB * c2;
-    uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
-    uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+  for (int r = 0; r < 2; ++r) {
+    const uint64_t pa = (uint64_t)PHILOX_MA * c0;
+    const uint64_t pb = (uint64_t)PHILOX_MB * c2;
+    const uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
+    c0 = n0;
+    c2 = n2;
+    k0 += PHILOX_WA;
+    k1 += PHILOX_WB;
+  }
+  // Rounds 2-9: both words per round are one 3-input xor each.
+#pragma unroll
+  for (int r = 2; r < 10; ++r) {
+    const uint64_t pa = (uint64_t)PHILOX_MA * c0;
+    const uint64_t pb = (uint64_t)PHILOX_MB * c2;
+    const uint32_t n0 = xor3_vvs((uint32_t)(pb >> 32), c1, k0);
+    const uint32_t n2 = xor3_vvs((uint32_t)(pa >> 32), c3, k1);
     c1 = (uint32_t)pb;
     c3 = (uint32_t)pa;
     c0 = n0;

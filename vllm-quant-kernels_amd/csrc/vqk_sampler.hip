@@ -13,19 +13,20 @@
 // scoring every element of a [32, 248320] batch is ALU-bound (~30 us).  The kernel prunes
 // exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
 // row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
-// A good L needs the whole row, so the work is three launches with no spinning or
-// cross-workgroup waits:
+// A good L needs the whole row, so the work is three launches with no spinning, no
+// cross-workgroup waits and no workspace initialisation:
 //   1. gumbel_cand_kernel streams the logits (256 threads x 64 floats per workgroup,
-//      coalesced 16-byte loads); greedy rows take their argmax here; sampled rows score
-//      one candidate per thread (its largest raw logit); each workgroup publishes its best
-//      with one 64-bit atomicMax on (orderable(y) << 32 | ~v) - largest y, then smallest v;
+//      coalesced 16-byte loads, about three instructions per element); greedy rows take
+//      their argmax here; sampled rows score one candidate per thread (its largest raw
+//      logit); each workgroup stores its best key (orderable(y) << 32 | ~v: largest y,
+//      then smallest v) and its blocks' largest admissible logits;
 //   2. gumbel_surv_kernel re-reads the sampled rows (recently streamed, so mostly served by
-//      the 256 MB last-level cache) in small slices, drops everything under the row's
-//      cutoff with one compare and scores the survivors through a per-workgroup LDS
-//      queue, 64 per wave-step;
-//   3. gumbel_finish_kernel turns each row key into the token and clears it.
-// On the BASELINE logits about 19% of the sampled elements of a B=32 batch survive, almost
-// all of them in the rows with the highest temperatures.
+//      the 256 MB last-level cache) in small slices, skips blocks under the row's cutoff,
+//      drops everything else under it with one compare and scores the survivors through a
+//      per-workgroup LDS queue, 64 per wave-step;
+//   3. gumbel_finish_kernel reduces each row's keys to the token.
+// On the BASELINE logits about a quarter of the sampled elements of a B=32 batch survive,
+// almost all of them in the rows with the highest temperatures.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,9 +52,10 @@ struct SmpArgs {
   int seed64;
   const float* thr;
   int64_t* out;
-  unsigned long long* keys;  // [B] row best key
-  uint32_t* bkeys;           // [B, nblk] orderable key of each 1024-logit block's largest
-                             // admissible logit (0: none)
+  unsigned long long* ckeys;  // [B, nchunks] best key of each candidate workgroup
+  unsigned long long* rkeys;  // [B] survivor pass's row key (cleared by the candidate pass)
+  uint32_t* bkeys;            // [B, nblk] orderable key of each 1024-logit block's largest
+                              // admissible logit (-inf: none)
   int nblk;
   int nchunks;
   int vec;                   // 16-byte loads allowed
@@ -68,24 +70,23 @@ struct RowParams {
   float thr;
 };
 
+// Every load is unconditional (an absent operand reads the first logit instead and the
+// value is then replaced), so the compiler issues them together behind one wait rather than
+// one wait per optional operand.
 __device__ __forceinline__ RowParams row_params(const SmpArgs& a, int row) {
+  const float* any = a.logits;
+  const float t = *(a.temp ? a.temp + row : any);
+  const float h = *(a.thr ? a.thr + row : any);
+  const uint32_t* sp = (const uint32_t*)a.seeds;
+  const uint32_t lo = sp[a.seed64 ? 2 * row : row];
+  const uint32_t hi = sp[a.seed64 ? 2 * row + 1 : row];
   RowParams p;
-  p.T = 1.0f;
-  p.greedy = true;
-  if (a.temp) {
-    p.T = a.temp[row];
-    p.greedy = p.T < GREEDY_EPS;
-  }
-  uint64_t s;
-  if (a.seed64) {
-    s = ((const uint64_t*)a.seeds)[row];
-  } else {
-    s = (uint64_t)(int64_t)((const int32_t*)a.seeds)[row];  // int32 -> uint64 sign-extends
-  }
-  p.k0 = (uint32_t)s;
-  p.k1 = (uint32_t)(s >> 32);
+  p.T = a.temp ? t : 1.0f;
+  p.greedy = a.temp ? (t < GREEDY_EPS) : true;
+  p.k0 = lo;
+  p.k1 = a.seed64 ? hi : (uint32_t)((int32_t)lo >> 31);  // int32 -> uint64 sign-extends
   p.has_thr = a.thr != nullptr;
-  p.thr = p.has_thr ? a.thr[row] : 0.f;
+  p.thr = p.has_thr ? h : 0.f;
   return p;
 }
 
@@ -98,8 +99,23 @@ __device__ __forceinline__ float score(const RowParams& p, float x, uint32_t v) 
   return a + gumbel_from_uniform(u);
 }
 
+// Score of an admissible, non-NaN logit of a sampled row: score() without the masks.
+__device__ __forceinline__ float score_sampled(const RowParams& p, float x, uint32_t v) {
+  const float a = x / p.T;
+  return a + gumbel_from_uniform(philox_uniform(philox_word0(v, p.k0, p.k1)));
+}
+
 __device__ __forceinline__ unsigned long long make_key(float y, uint32_t v) {
   return ((unsigned long long)orderable(y) << 32) | (unsigned long long)(~v);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)k, off);
+    k = o > k ? o : k;
+  }
+  return k;
 }
 
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
@@ -111,11 +127,12 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
   return k;
 }
 
-// Cross-workgroup protocol.  Only device-scope atomics on the workspace are used, relaxed:
-// acquire/release fences would write back and invalidate the L2 of the issuing XCD
-// (buffer_wbl2 / buffer_inv), which costs far more than the whole reduction.  The ordering
-// that matters is the one between launches, which the launch boundaries give: every atomic
-// of a launch is performed before the next launch reads the keys.
+// Cross-workgroup protocol.  Candidate workgroups store to slots of their own; survivor
+// workgroups that beat the candidates use one relaxed device-scope atomicMax on the row
+// key (acquire/release fences would write back and invalidate the L2 of the issuing XCD,
+// which costs far more than the whole reduction).  The ordering that matters is the one
+// between launches, which the launch boundaries give: every store and atomic of a launch
+// is performed before the next launch reads them.
 __device__ __forceinline__ unsigned long long ld_relaxed_u64(unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -178,72 +195,95 @@ __device__ __forceinline__ void load_slice(const float* rowp, int base, int tid,
   }
 }
 
-// Launch 1 (streams every logit once): 256 threads x 64 floats per workgroup.  Greedy rows:
-// each thread keeps its argmax of y = (admissible ? x : -inf).  Sampled rows: each thread
-// keeps its largest admissible raw logit and scores it (one Philox per 64 elements); a thread
-// with no admissible element offers its first element as -inf.  The workgroup's best key goes
-// to the row with one fire-and-forget 64-bit atomicMax.
+// v_max3_f32 / v_max_f32 as written: fmaxf would first quiet each operand (one more
+// instruction per element) for IEEE NaN semantics.  Only NaN-free lanes use these; a lane
+// holding a NaN takes the key form.
+__device__ __forceinline__ float max3_nn(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_nn(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// Order-preserving key of a NaN-free float (-0.0 ranks just below +0.0, which no consumer
+// of these keys distinguishes).
+__device__ __forceinline__ uint32_t orderable_nn(float y) {
+  const uint32_t b = bits_f32(y);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+
+// Launch 1 (streams every logit once): 256 threads x 64 floats per workgroup.  Each
+// thread masks its inadmissible elements (below the top-k threshold, past the row end) to
+// -inf and takes, in float arithmetic, the maximum of each 4-element group (its share of
+// one 1024-logit block) and of all 64, then the first index holding that maximum: about
+// three instructions per element.  A lane with a NaN (which must rank above everything)
+// redoes its slice on order-preserving keys instead.  Greedy rows: the thread's best is
+// (max, first index).  Sampled rows: the thread scores its largest admissible logit (one
+// Philox per 64 elements) and the workgroup also stores the largest admissible logit of
+// each of its 16 blocks for the survivor pass.  The workgroup's best key
+// (orderable(y) << 32 | ~v: largest y, then smallest v) goes to its own slot: no atomics.
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   __shared__ unsigned long long red[SMP_THREADS / 64];
   __shared__ uint32_t bred[SMP_THREADS / 64][16];
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const int base = blockIdx.x * SMP_CHUNK;
-  const bool full = a.vec && base + SMP_CHUNK <= a.V;
+  const bool inrange = base + SMP_CHUNK <= a.V;
   float xv[SMP_EPT];
-  load_slice(rowp, base, tid, a.V, full, xv);
+  load_slice(rowp, base, tid, a.V, a.vec && inrange, xv);
   const RowParams p = row_params(a, row);
+  // the survivor pass accumulates into the row key; cleared here, one launch ahead of it
+  if (blockIdx.x == 0 && tid == 0) a.rkeys[row] = 0ull;
   const float NEG_INF = -__builtin_inff();
-  const float thr = p.has_thr ? p.thr : NEG_INF;  // x < thr is masked (NaN is not)
-  // One pass: the thread's best key (greedy: y itself; sampled: the raw logit, which ranks
-  // the candidates) and the best key of each of its 16 element groups (group i of every
-  // thread is 1024-logit block i of the slice).  Inadmissible elements count as -inf, out
-  // of range ones as key 0, below every real key.
-  uint32_t km = 0u;
-  int qm = -1;
-  uint32_t mb[16];
-  bool slow = !full;
-  if (full) {
-    // Fast form in float compares: strict > keeps the first index and treats -0 == +0;
-    // NaN (which must rank above everything) only raises a flag that sends the thread to
-    // the key form below.
-    float m = NEG_INF, mf[16];
-    int qf = 0;
-    bool nan = false;
+  if (p.has_thr) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mf[i] = NEG_INF;
-#pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
-      const float x = xv[q] < thr ? NEG_INF : xv[q];
-      nan = nan || (x != x);
-      const bool b = x > m;
-      m = b ? x : m;
-      qf = b ? q : qf;
-      mf[q >> 2] = fmaxf(mf[q >> 2], x);
-    }
-    if (!nan) {
-      km = orderable(m);
-      qm = qf;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mb[i] = orderable(mf[i]);
-    }
-    slow = nan;
+    for (int q = 0; q < SMP_EPT; ++q) xv[q] = xv[q] < p.thr ? NEG_INF : xv[q];  // NaN stays
   }
-  if (slow) {
-    // Key form: orderable keys (NaN on top); out-of-range elements are key 0.
+  if (!inrange) {
+#pragma unroll
+    for (int q = 0; q < SMP_EPT; ++q) xv[q] = slice_v(base, tid, q) < a.V ? xv[q] : NEG_INF;
+  }
+  // group maxima and the NaN test in load order, so each group waits only for its own load
+  bool nan = false;
+  float mf[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    nan |= __builtin_isunordered(xv[4 * i], xv[4 * i + 1]) | __builtin_isunordered(xv[4 * i + 2], xv[4 * i + 3]);
+    mf[i] = max_nn(max3_nn(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2]), xv[4 * i + 3]);
+  }
+  uint32_t km, mb[16];
+  int qm;
+  if (!nan) {
+    float m4[6];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) m4[i] = max3_nn(mf[3 * i], mf[3 * i + 1], mf[3 * i + 2]);
+    m4[5] = mf[15];
+    const float m = max3_nn(max3_nn(m4[0], m4[1], m4[2]), max3_nn(m4[3], m4[4], m4[5]), m4[5]);
+    int qf = 0;
+#pragma unroll
+    for (int q = SMP_EPT - 1; q >= 0; --q) qf = (xv[q] == m) ? q : qf;
+    km = orderable_nn(m);
+    qm = qf;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mb[i] = orderable_nn(mf[i]);
+  } else {
     km = 0u;
-    qm = -1;
+    qm = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) mb[i] = 0u;
 #pragma unroll
     for (int q = 0; q < SMP_EPT; ++q) {
-      const uint32_t k = slice_v(base, tid, q) < a.V ? orderable(xv[q] < thr ? NEG_INF : xv[q]) : 0u;
+      const uint32_t k = orderable(xv[q]);
       take_max(k, q, km, qm);
       mb[q >> 2] = k > mb[q >> 2] ? k : mb[q >> 2];
     }
   }
+  // a thread whose first element is past the row end has none in range
   unsigned long long best = 0ull;
-  if (qm >= 0) {
+  if (slice_v(base, tid, 0) < a.V) {
     const uint32_t v = (uint32_t)slice_v(base, tid, qm);
     float y = from_orderable(km);
     if (!p.greedy && y > NEG_INF) y = score(p, y, v);
@@ -252,16 +292,20 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   if (!p.greedy) {
     // Block maxima for the survivor pass.  A butterfly that halves the values at each of
     // its first four steps leaves lane l with the wave's maximum of block (l >> 2) & 15.
+    // At each exchange the lanes with `bit` set swap the pair (a masked xor swap, which the
+    // compiler cannot turn into a dynamically indexed register select), so that every lane
+    // keeps mb[j] and sends mb[j + half].
 #pragma unroll
     for (int step = 0; step < 4; ++step) {
       const int half = 8 >> step, bit = 32 >> step;
-      const bool up = (lane & bit) != 0;
+      const uint32_t upm = (lane & bit) ? 0xFFFFFFFFu : 0u;
 #pragma unroll
       for (int j = 0; j < half; ++j) {
-        const uint32_t send = up ? mb[j] : mb[j + half];
-        const uint32_t keep = up ? mb[j + half] : mb[j];
-        const uint32_t got = (uint32_t)__shfl_xor((int)send, bit);
-        mb[j] = got > keep ? got : keep;
+        const uint32_t t = (mb[j] ^ mb[j + half]) & upm;
+        mb[j] ^= t;
+        mb[j + half] ^= t;
+        const uint32_t got = (uint32_t)__shfl_xor((int)mb[j + half], bit);
+        mb[j] = got > mb[j] ? got : mb[j];
       }
     }
 #pragma unroll
@@ -280,64 +324,62 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
     }
   }
   const unsigned long long gb = block_max_u64(best, red);
-  if (tid == 0) amax_u64(&a.keys[row], gb);
+  if (tid == 0) a.ckeys[(int64_t)row * a.nchunks + blockIdx.x] = gb;
 }
 
-// Launch 2 (sampled rows only; greedy rows return at once).  The row key holds every
-// candidate, a score L the winner is >= to.  Since G <= GUMBEL_MAX for every Philox word
-// and rounding is monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is
-// one compare against a per-row raw-logit cutoff; whole 1024-logit blocks whose largest
-// admissible logit is under the cutoff are skipped unread.  Survivors cluster in the rows
-// with high temperature, so this pass uses small slices (EPT elements per thread): many
-// short workgroups let the dispatcher spread one hot row over every CU.  A workgroup
-// touches the row key only if it found a better score than L, which is rare.
+// The score part (high word) of the row's candidate keys: lane l reads slot l (and l + 64,
+// ... past 64 slots); reduce with wave_max_u32.
+__device__ __forceinline__ uint32_t row_cand_score(const SmpArgs& a, int row, int lane) {
+  const uint32_t* s = (const uint32_t*)(a.ckeys + (int64_t)row * a.nchunks) + 1;
+  uint32_t k = lane < a.nchunks ? s[2 * lane] : 0u;  // no wait here unless V > 1M
+  for (int c = lane + 64; c < a.nchunks; c += 64) k = s[2 * c] > k ? s[2 * c] : k;
+  return k;
+}
+
+// The row's best candidate key: the maximum of the candidate pass's slots, reduced over
+// one wave (every lane returns it).
+__device__ __forceinline__ unsigned long long row_cand_key(const SmpArgs& a, int row, int lane) {
+  const unsigned long long* s = a.ckeys + (int64_t)row * a.nchunks;
+  unsigned long long k = lane < a.nchunks ? s[lane] : 0ull;  // no wait here unless V > 1M
+  for (int c = lane + 64; c < a.nchunks; c += 64) k = s[c] > k ? s[c] : k;
+  return k;
+}
+
+// Launch 2 (sampled rows only; greedy rows return at once).  The candidates give a score L
+// the winner is >= to.  Since G <= GUMBEL_MAX for every Philox word and rounding is
+// monotone, x with fl(fl(x/T) + GUMBEL_MAX) < L cannot win; the test is one compare
+// against a per-row raw-logit cutoff; whole 1024-logit blocks whose largest admissible
+// logit is under the cutoff are skipped unread.  Survivors cluster in the rows with high
+// temperature, so this pass uses small slices (EPT elements per thread): many short
+// workgroups let the dispatcher spread one hot row over every CU.  A workgroup touches the
+// row key only if it found a better score than L, which is rare.
 
 template <int EPT>
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   constexpr int CAP = SMP_THREADS * EPT;  // every element of the slice may survive
-  __shared__ unsigned long long red[SMP_THREADS / 64];
+  constexpr int NB = EPT / 4;             // 1024-logit blocks per slice
   __shared__ float qx[CAP];
   __shared__ uint32_t qv[CAP];
-  __shared__ int qn;
+  __shared__ int qn, sgo;
+  __shared__ float sxc, sL;
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-  // every per-row and per-block value this workgroup needs is loaded at once, so the
-  // decision to skip costs one memory latency
-  constexpr int NB = EPT / 4;  // 1024-logit blocks per slice
-  const unsigned long long lk = ld_relaxed_u64(&a.keys[row]);
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const int base = blockIdx.x * CAP;
+  const bool ragged = !(base + CAP <= a.V);
+  // Everything the workgroup needs is requested at once - the row's candidate keys (wave 0,
+  // which alone derives the row's cutoff), the slice's block keys and, before it is known
+  // whether the slice survives, its logits (a re-read served by the last-level cache) - so
+  // a workgroup costs one memory latency.
+  uint32_t lh = 0u;
+  if (tid < 64) lh = row_cand_score(a, row, lane);
   uint32_t bk[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int blk = blockIdx.x * NB + i;
-    bk[i] = blk < a.nblk ? a.bkeys[(int64_t)row * a.nblk + blk] : 0u;
+    bk[i] = blk < a.nblk ? a.bkeys[(int64_t)row * a.nblk + blk] : 0x007FFFFFu;  // -inf: none
   }
-  const RowParams p = row_params(a, row);
-  if (p.greedy) return;
-  const float NEG_INF = -__builtin_inff();
-  const float L = from_orderable((uint32_t)(lk >> 32));
-  float xc = NEG_INF;
-  if (L > NEG_INF && L == L) {
-    float c = (L - GUMBEL_MAX) * p.T;
-    for (int it = 0; it < 16; ++it) {
-      if ((c / p.T) + GUMBEL_MAX < L) {
-        xc = c;
-        break;
-      }
-      c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
-    }
-  }
-  // skip the slice without reading it when no block of it has an admissible logit > xc
-  // (wave-uniform: every thread reads the same keys)
-  {
-    bool any = false;
-#pragma unroll
-    for (int i = 0; i < NB; ++i) any = any || (bk[i] != 0u && !(from_orderable(bk[i]) <= xc));
-    if (!any) return;
-  }
-  const float* rowp = a.logits + (int64_t)row * a.ld;
-  const int base = blockIdx.x * (SMP_THREADS * EPT);
-  const bool full = a.vec && base + SMP_THREADS * EPT <= a.V;
   float xv[EPT];
-  if (full) {
+  if (a.vec && !ragged) {
 #pragma unroll
     for (int i = 0; i < EPT / 4; ++i) {
       const v4f t = *(const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4);
@@ -348,56 +390,102 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
-      xv[q] = rowp[v < a.V ? v : a.V - 1];
+    for (int q = 0; q < EPT; ++q) xv[q] = rowp[min(slice_v(base, tid, q), a.V - 1)];
+  }
+  const RowParams p = row_params(a, row);
+  if (p.greedy) return;
+  const float NEG_INF = -__builtin_inff();
+  if (tid < 64) {
+    // L: the best candidate score of the row.  A NaN there means the row holds a NaN,
+    // whose first occurrence the candidates already hold and nothing can beat.
+    const float L = from_orderable(wave_max_u32(lh));
+    float xc = NEG_INF;
+    if (L > NEG_INF && L == L) {
+      float c = (L - GUMBEL_MAX) * p.T;
+      for (int it = 0; it < 16; ++it) {
+        if ((c / p.T) + GUMBEL_MAX < L) {
+          xc = c;
+          break;
+        }
+        c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
+      }
+    }
+    // the slice is needed only if some block of it has an admissible logit > xc
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) any = any || !(from_orderable(bk[i]) <= xc);
+    if (lane == 0) {
+      sxc = xc;
+      sL = L;
+      qn = 0;
+      sgo = (any && L == L) ? 1 : 0;
     }
   }
-  // Survivors of the whole workgroup go to one LDS queue (one LDS atomic per wave and
-  // element step reserves the wave's run), then every thread scores queue entries tid,
-  // tid + 256, ...: n survivors cost ceil(n / 64) wave-scores however they are spread.
-  if (tid == 0) qn = 0;
   __syncthreads();
+  if (!sgo) return;
+  const float xc = sxc, L = sL;
+  // Survivors of the whole workgroup go to one LDS queue: each wave counts its survivors
+  // of every step (ballots), reserves its run with one LDS atomic and writes them in
+  // order; then every thread scores entries tid, tid + 256, ...: n survivors cost
+  // ceil(n / 64) wave-scores however they are spread over the slice.
+  unsigned long long bm[EPT];
+  int cnt = 0;
 #pragma unroll
   for (int q = 0; q < EPT; ++q) {
-    const int v = base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
-    const bool s = v < a.V && !(p.has_thr && !(xv[q] >= p.thr)) && !(xv[q] <= xc);
-    const unsigned long long m = __ballot(s);
-    if (m) {
-      int wbase = 0;
-      if (lane == 0)
-        wbase = __hip_atomic_fetch_add(&qn, (int)__popcll(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      wbase = __shfl(wbase, 0);
-      if (s) {
-        const int pos = wbase + (int)__popcll(m & ((1ull << lane) - 1ull));
+    bool s = !(xv[q] <= xc);
+    if (p.has_thr) s = s && xv[q] >= p.thr;
+    if (ragged) s = s && slice_v(base, tid, q) < a.V;
+    bm[q] = __ballot(s);
+    cnt += (int)__popcll(bm[q]);
+  }
+  if (cnt) {
+    int wbase = 0;
+    if (lane == 0) wbase = __hip_atomic_fetch_add(&qn, cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    wbase = __builtin_amdgcn_readfirstlane(wbase);
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      if ((bm[q] >> lane) & 1ull) {
+        const int pos = wbase + (int)__popcll(bm[q] & below);
         qx[pos] = xv[q];
-        qv[pos] = (uint32_t)v;
+        qv[pos] = (uint32_t)slice_v(base, tid, q);
       }
+      wbase += (int)__popcll(bm[q]);
     }
   }
   __syncthreads();
   const int n = qn;
-  unsigned long long best = 0ull;
+  // Running maximum in float with the smallest index on ties (no survivor is NaN: NaN rows
+  // stopped above; -0.0 == +0.0 as the order-preserving key has it).
+  float by = NEG_INF;
+  uint32_t bv = 0xFFFFFFFFu;  // none yet
   for (int i = tid; i < n; i += SMP_THREADS) {
     const float x = qx[i];
     const uint32_t v = qv[i];
-    const unsigned long long k = make_key(score(p, x, v), v);
-    best = (k > best) ? k : best;
+    const float y = score_sampled(p, x, v);
+    const bool b = (y > by) || (y == by && v < bv);
+    by = b ? y : by;
+    bv = b ? v : bv;
   }
-  const unsigned long long gb = block_max_u64(best, red);
-  if (tid == 0 && gb > lk) amax_u64(&a.keys[row], gb);
+  // beating the candidates (score >= L) is rare: only then a wave reduction and an atomic
+  if (__ballot(bv != 0xFFFFFFFFu && by >= L)) {
+    const unsigned long long gb = wave_max_u64(bv != 0xFFFFFFFFu ? make_key(by, bv) : 0ull);
+    if (lane == 0) amax_u64(&a.rkeys[row], gb);
+  }
 }
 
-// Launch 3: the token of each row from its key; the whole workspace (keys and block keys)
-// is cleared for the next call, whatever its batch size.
-__global__ void gumbel_finish_kernel(SmpArgs a) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < a.B) {
-    const unsigned long long k = ld_relaxed_u64(&a.keys[i]);
-    a.out[i] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
-    __hip_atomic_store(&a.keys[i], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Launch 3: one wave per row reduces the candidate slots and the survivor pass's row key
+// to the token.
+__global__ void __launch_bounds__(256) gumbel_finish_kernel(SmpArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= a.B) return;
+  unsigned long long k = row_cand_key(a, row, lane);
+  if (lane == 0) {
+    const unsigned long long r = ld_relaxed_u64(&a.rkeys[row]);
+    k = r > k ? r : k;
   }
-  if (i < a.B * a.nblk) a.bkeys[i] = 0u;
+  k = wave_max_u64(k);
+  if (lane == 0) a.out[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
 }
 
 // Debug kernel: y for every element.
@@ -414,10 +502,14 @@ __global__ void gumbel_scores_kernel(SmpArgs a) {
 using namespace vqk;
 
 static int64_t gumbel_nblk(int64_t V) { return (V + 1023) / 1024; }
+static int64_t gumbel_nchunks(int64_t V) { return (V + SMP_CHUNK - 1) / SMP_CHUNK; }
 
+// ckeys [B, nchunks] u64, rkeys [B] u64, bkeys [B, nblk] u32: every launch writes each
+// value before reading it, so the workspace needs no initialisation.
 extern "C" int64_t vqk_gumbel_workspace_size(int64_t B, int64_t V) {
   if (B < 0 || V < 0) return 0;
-  return B * (int64_t)sizeof(unsigned long long) + B * gumbel_nblk(V) * (int64_t)sizeof(uint32_t) + 16;
+  return B * (gumbel_nchunks(V) + 1) * (int64_t)sizeof(unsigned long long) +
+         B * gumbel_nblk(V) * (int64_t)sizeof(uint32_t) + 16;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
@@ -448,14 +540,14 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.seed64 = seed_is_64bit ? 1 : 0;
   a.thr = topk_thr;
   a.out = out;
-  a.keys = (unsigned long long*)workspace;
-  a.bkeys = (uint32_t*)((char*)workspace + B * sizeof(unsigned long long));
   a.nblk = (int)gumbel_nblk(V);
-  a.nchunks = (int)((V + SMP_CHUNK - 1) / SMP_CHUNK);
+  a.nchunks = (int)gumbel_nchunks(V);
+  a.ckeys = (unsigned long long*)workspace;
+  a.rkeys = a.ckeys + B * (int64_t)a.nchunks;
+  a.bkeys = (uint32_t*)(a.rkeys + B);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
   hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                      (hipStream_t)stream, a);
-  // survivor pass: 1024 logits per workgroup for up to ~8M elements, else 4096
   // survivor slices: 1024 logits per workgroup for small batches (more workgroups to spread
   // a hot row over), 2048 beyond ~2M elements (measured best at B = 32 and 128)
   if (B * V <= ((int64_t)2 << 20)) {
@@ -465,8 +557,7 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
     const int ns = (int)((V + SMP_THREADS * 8 - 1) / (SMP_THREADS * 8));
     hipLaunchKernelGGL(gumbel_surv_kernel<8>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
-  const int64_t nfin = B * (int64_t)a.nblk;
-  hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((nfin + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }

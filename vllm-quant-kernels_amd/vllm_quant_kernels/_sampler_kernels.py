@@ -27,15 +27,15 @@ _workspaces: dict = {}
 
 
 def _workspace(device: torch.device, stream: int, B: int, V: int) -> torch.Tensor:
-    """Per (device, stream) zero-initialised workspace; the kernel leaves it zeroed again,
-    so it is cleared only when first created or grown.  Launches on one stream are ordered,
+    """Per (device, stream) workspace, grown as needed.  The kernels write every value
+    before reading it, so it needs no initialisation.  Launches on one stream are ordered,
     so sharing it among them is safe; different streams get different workspaces."""
     need = int(_lib.load().vqk_gumbel_workspace_size(B, V))
     key = (device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < need:
-            ws = torch.zeros(max(need, 4096), dtype=torch.uint8, device=device)
+            ws = torch.empty(max(need, 4096), dtype=torch.uint8, device=device)
             _workspaces[key] = ws
     return ws
 
