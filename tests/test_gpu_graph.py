@@ -29,8 +29,8 @@ def _capture(fn, warm):
     return g, out
 
 
-def test_sampler_graph_replays_match_eager():
-    B = 32
+@pytest.mark.parametrize("B", [4, 32])  # single-pass and two-pass forms
+def test_sampler_graph_replays_match_eager(B):
     logits, temp, seeds = syn.sampler_inputs(B)
     eager = S_.fused_gumbel_sample(logits, temp, seeds).clone()
     g, out = _capture(lambda: S_.fused_gumbel_sample(logits, temp, seeds), 2)

@@ -13,8 +13,8 @@
 // scoring every element of a [32, 248320] batch is ALU-bound (~30 us).  The kernel prunes
 // exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
 // row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
-// A good L needs the whole row, so the work is three launches with no spinning, no
-// cross-workgroup waits and no workspace initialisation:
+// A good L needs the whole row, so batches of more than ~2M logits take three launches
+// with no spinning, no cross-workgroup waits and no workspace initialisation:
 //   1. gumbel_cand_kernel streams the logits (256 threads x 64 floats per workgroup,
 //      coalesced 16-byte loads, about three instructions per element); greedy rows take
 //      their argmax here; sampled rows score one candidate per thread (its largest raw
@@ -25,8 +25,10 @@
 //      drops everything else under it with one compare and scores the survivors through a
 //      per-workgroup LDS queue, 64 per wave-step;
 //   3. gumbel_finish_kernel reduces each row's keys to the token.
-// On the BASELINE logits about a quarter of the sampled elements of a B=32 batch survive,
-// almost all of them in the rows with the highest temperatures.
+// Smaller batches are a few workgroup latencies long, so launches dominate there: they
+// take gumbel_local_kernel (one pass, each wave pruned against its own best candidate)
+// and the finish.  On the BASELINE logits about a fifth of the sampled elements of a B=32
+// batch survive, almost all of them in the rows with the highest temperatures.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,8 +41,9 @@ namespace vqk {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int SMP_THREADS = 256;
-constexpr int SMP_EPT = 64;                               // elements per thread
-constexpr int SMP_CHUNK = SMP_THREADS * SMP_EPT;          // elements per workgroup
+// candidate pass: 64 elements per thread (16 for small batches, which gives more, shorter
+// workgroups); its smallest chunk bounds the number of candidate slots per row
+constexpr int SMP_MIN_CHUNK = SMP_THREADS * 4;
 constexpr float GREEDY_EPS = 1e-5f;
 
 struct SmpArgs {
@@ -175,11 +178,12 @@ __device__ __forceinline__ void take_max(uint32_t k, int q, uint32_t& km, int& q
 __device__ __forceinline__ int slice_v(int base, int tid, int q) {
   return base + ((q >> 2) * SMP_THREADS + tid) * 4 + (q & 3);
 }
+template <int EPT>
 __device__ __forceinline__ void load_slice(const float* rowp, int base, int tid, int V, bool full,
-                                           float (&xv)[SMP_EPT]) {
+                                           float (&xv)[EPT]) {
   if (full) {
 #pragma unroll
-    for (int i = 0; i < SMP_EPT / 4; ++i) {
+    for (int i = 0; i < EPT / 4; ++i) {
       const v4f t = *(const v4f*)(rowp + base + (i * SMP_THREADS + tid) * 4);
       xv[4 * i] = t.x;
       xv[4 * i + 1] = t.y;
@@ -188,7 +192,7 @@ __device__ __forceinline__ void load_slice(const float* rowp, int base, int tid,
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
+    for (int q = 0; q < EPT; ++q) {
       const int v = slice_v(base, tid, q);
       xv[q] = rowp[v < V ? v : V - 1];
     }
@@ -225,57 +229,61 @@ __device__ __forceinline__ uint32_t orderable_nn(float y) {
 // Philox per 64 elements) and the workgroup also stores the largest admissible logit of
 // each of its 16 blocks for the survivor pass.  The workgroup's best key
 // (orderable(y) << 32 | ~v: largest y, then smallest v) goes to its own slot: no atomics.
+template <int EPT>
 __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
+  constexpr int CHUNK = SMP_THREADS * EPT;
+  constexpr int NB = EPT / 4;                      // 1024-logit blocks per chunk
+  constexpr int LOGNB = NB == 16 ? 4 : (NB == 8 ? 3 : (NB == 4 ? 2 : (NB == 2 ? 1 : 0)));
+  static_assert((1 << LOGNB) == NB, "EPT / 4 must be a power of two");
   __shared__ unsigned long long red[SMP_THREADS / 64];
-  __shared__ uint32_t bred[SMP_THREADS / 64][16];
+  __shared__ uint32_t bred[SMP_THREADS / 64][NB];
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const float* rowp = a.logits + (int64_t)row * a.ld;
-  const int base = blockIdx.x * SMP_CHUNK;
-  const bool inrange = base + SMP_CHUNK <= a.V;
-  float xv[SMP_EPT];
-  load_slice(rowp, base, tid, a.V, a.vec && inrange, xv);
+  const int base = blockIdx.x * CHUNK;
+  const bool inrange = base + CHUNK <= a.V;
+  float xv[EPT];
+  load_slice<EPT>(rowp, base, tid, a.V, a.vec && inrange, xv);
   const RowParams p = row_params(a, row);
   // the survivor pass accumulates into the row key; cleared here, one launch ahead of it
   if (blockIdx.x == 0 && tid == 0) a.rkeys[row] = 0ull;
   const float NEG_INF = -__builtin_inff();
   if (p.has_thr) {
 #pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) xv[q] = xv[q] < p.thr ? NEG_INF : xv[q];  // NaN stays
+    for (int q = 0; q < EPT; ++q) xv[q] = xv[q] < p.thr ? NEG_INF : xv[q];  // NaN stays
   }
   if (!inrange) {
 #pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) xv[q] = slice_v(base, tid, q) < a.V ? xv[q] : NEG_INF;
+    for (int q = 0; q < EPT; ++q) xv[q] = slice_v(base, tid, q) < a.V ? xv[q] : NEG_INF;
   }
   // group maxima and the NaN test in load order, so each group waits only for its own load
   bool nan = false;
-  float mf[16];
+  float mf[NB];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NB; ++i) {
     nan |= __builtin_isunordered(xv[4 * i], xv[4 * i + 1]) | __builtin_isunordered(xv[4 * i + 2], xv[4 * i + 3]);
     mf[i] = max_nn(max3_nn(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2]), xv[4 * i + 3]);
   }
-  uint32_t km, mb[16];
+  uint32_t km, mb[NB];
   int qm;
   if (!nan) {
-    float m4[6];
+    float m = mf[0];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) m4[i] = max3_nn(mf[3 * i], mf[3 * i + 1], mf[3 * i + 2]);
-    m4[5] = mf[15];
-    const float m = max3_nn(max3_nn(m4[0], m4[1], m4[2]), max3_nn(m4[3], m4[4], m4[5]), m4[5]);
+    for (int i = 1; i + 1 < NB; i += 2) m = max3_nn(m, mf[i], mf[i + 1]);
+    if ((NB & 1) == 0 && NB > 1) m = max_nn(m, mf[NB - 1]);
     int qf = 0;
 #pragma unroll
-    for (int q = SMP_EPT - 1; q >= 0; --q) qf = (xv[q] == m) ? q : qf;
+    for (int q = EPT - 1; q >= 0; --q) qf = (xv[q] == m) ? q : qf;
     km = orderable_nn(m);
     qm = qf;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mb[i] = orderable_nn(mf[i]);
+    for (int i = 0; i < NB; ++i) mb[i] = orderable_nn(mf[i]);
   } else {
     km = 0u;
     qm = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mb[i] = 0u;
+    for (int i = 0; i < NB; ++i) mb[i] = 0u;
 #pragma unroll
-    for (int q = 0; q < SMP_EPT; ++q) {
+    for (int q = 0; q < EPT; ++q) {
       const uint32_t k = orderable(xv[q]);
       take_max(k, q, km, qm);
       mb[q >> 2] = k > mb[q >> 2] ? k : mb[q >> 2];
@@ -291,13 +299,15 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   }
   if (!p.greedy) {
     // Block maxima for the survivor pass.  A butterfly that halves the values at each of
-    // its first four steps leaves lane l with the wave's maximum of block (l >> 2) & 15.
-    // At each exchange the lanes with `bit` set swap the pair (a masked xor swap, which the
-    // compiler cannot turn into a dynamically indexed register select), so that every lane
-    // keeps mb[j] and sends mb[j + half].
+    // its first LOGNB steps leaves lane l with the wave's maximum over the lanes sharing
+    // bits 5..SH of l of block (l >> SH) & (NB - 1); the remaining steps reduce over the
+    // low SH bits.  At each halving exchange the lanes with `bit` set swap the pair (a
+    // masked xor swap, which the compiler cannot turn into a dynamically indexed register
+    // select), so that every lane keeps mb[j] and sends mb[j + half].
+    constexpr int SH = 6 - LOGNB;
 #pragma unroll
-    for (int step = 0; step < 4; ++step) {
-      const int half = 8 >> step, bit = 32 >> step;
+    for (int step = 0; step < LOGNB; ++step) {
+      const int half = NB >> (step + 1), bit = 32 >> step;
       const uint32_t upm = (lane & bit) ? 0xFFFFFFFFu : 0u;
 #pragma unroll
       for (int j = 0; j < half; ++j) {
@@ -309,14 +319,14 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
       }
     }
 #pragma unroll
-    for (int bit = 2; bit >= 1; bit >>= 1) {
+    for (int bit = 1 << (SH - 1); bit >= 1; bit >>= 1) {
       const uint32_t got = (uint32_t)__shfl_xor((int)mb[0], bit);
       mb[0] = got > mb[0] ? got : mb[0];
     }
-    if ((lane & 3) == 0) bred[tid >> 6][lane >> 2] = mb[0];
+    if ((lane & ((1 << SH) - 1)) == 0) bred[tid >> 6][lane >> SH] = mb[0];
     __syncthreads();
-    const int blk = blockIdx.x * 16 + tid;
-    if (tid < 16 && blk < a.nblk) {
+    const int blk = blockIdx.x * NB + tid;
+    if (tid < NB && blk < a.nblk) {
       uint32_t k = bred[0][tid];
 #pragma unroll
       for (int w = 1; w < SMP_THREADS / 64; ++w) k = bred[w][tid] > k ? bred[w][tid] : k;
@@ -325,6 +335,25 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_cand_kernel(SmpArgs a) {
   }
   const unsigned long long gb = block_max_u64(best, red);
   if (tid == 0) a.ckeys[(int64_t)row * a.nchunks + blockIdx.x] = gb;
+}
+
+// The raw-logit cutoff of a sampled row whose winner scores >= L: every x <= xc has
+// fl(fl(x/T) + GUMBEL_MAX) < L, so its score (x/T + G with G <= GUMBEL_MAX, rounding
+// monotone) is < L and it cannot win.  Starts from the real-arithmetic bound and steps
+// down until the rounded test holds; -inf (nothing pruned) when L is -inf or NaN.
+__device__ __forceinline__ float raw_cutoff(float L, float T) {
+  float xc = -__builtin_inff();
+  if (L > xc && L == L) {
+    float c = (L - GUMBEL_MAX) * T;
+    for (int it = 0; it < 16; ++it) {
+      if ((c / T) + GUMBEL_MAX < L) {
+        xc = c;
+        break;
+      }
+      c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
+    }
+  }
+  return xc;
 }
 
 // The score part (high word) of the row's candidate keys: lane l reads slot l (and l + 64,
@@ -399,17 +428,7 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
     // L: the best candidate score of the row.  A NaN there means the row holds a NaN,
     // whose first occurrence the candidates already hold and nothing can beat.
     const float L = from_orderable(wave_max_u32(lh));
-    float xc = NEG_INF;
-    if (L > NEG_INF && L == L) {
-      float c = (L - GUMBEL_MAX) * p.T;
-      for (int it = 0; it < 16; ++it) {
-        if ((c / p.T) + GUMBEL_MAX < L) {
-          xc = c;
-          break;
-        }
-        c = c - fmaxf(fabsf(c) * 4.76837158e-7f, 1e-30f);
-      }
-    }
+    const float xc = raw_cutoff(L, p.T);
     // the slice is needed only if some block of it has an admissible logit > xc
     bool any = false;
 #pragma unroll
@@ -474,6 +493,82 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   }
 }
 
+// Single pass for small batches (up to ~2M logits), where three launches of a few
+// latencies each would dominate: 256 threads x 4 logits per workgroup; each wave takes its
+// largest admissible logit (first index) as its candidate, scores it (L), prunes its other
+// logits with raw_cutoff(L) and scores the rest through a per-wave LDS queue.  Exact for
+// the same reason as the two-pass form: a pruned logit scores < L <= the row's best.
+// Greedy rows keep the wave's argmax; a NaN (ranked above everything) wins at its first
+// occurrence and needs no scoring.  Each workgroup stores its best key in its slot.
+__global__ void __launch_bounds__(SMP_THREADS) gumbel_local_kernel(SmpArgs a) {
+  constexpr int EPT = 4, CHUNK = SMP_THREADS * EPT;
+  __shared__ float qx[SMP_THREADS * EPT];
+  __shared__ uint32_t qv[SMP_THREADS * EPT];
+  __shared__ unsigned long long red[SMP_THREADS / 64];
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const int base = blockIdx.x * CHUNK;
+  const bool inrange = base + CHUNK <= a.V;
+  float xv[EPT];
+  load_slice<EPT>(rowp, base, tid, a.V, a.vec && inrange, xv);
+  const RowParams p = row_params(a, row);
+  if (blockIdx.x == 0 && tid == 0) a.rkeys[row] = 0ull;  // unused by this path: finish reads 0
+  const float NEG_INF = -__builtin_inff();
+  // the thread's largest admissible logit on order-preserving keys (NaN on top)
+  uint32_t km = 0u;
+  int qm = -1;
+#pragma unroll
+  for (int q = 0; q < EPT; ++q) {
+    if (p.has_thr) xv[q] = xv[q] < p.thr ? NEG_INF : xv[q];  // NaN stays
+    if (slice_v(base, tid, q) < a.V) take_max(orderable(xv[q]), q, km, qm);
+  }
+  const unsigned long long tk =
+      qm >= 0 ? (((unsigned long long)km << 32) | (unsigned long long)(~(uint32_t)slice_v(base, tid, qm))) : 0ull;
+  unsigned long long best = wave_max_u64(tk);  // greedy rows: the wave's argmax
+  const float xm = from_orderable((uint32_t)(best >> 32));
+  if (!p.greedy && best != 0ull && xm == xm) {
+    const uint32_t vm = ~(uint32_t)best;
+    const float L = xm > NEG_INF ? score_sampled(p, xm, vm) : NEG_INF;
+    best = make_key(L, vm);
+    const float xc = raw_cutoff(L, p.T);
+    // survivors: in range, admissible (masked ones are -inf <= xc), above the cutoff, not
+    // the candidate itself; compacted into this wave's quarter of the queue
+    float* wx = qx + wave * 64 * EPT;
+    uint32_t* wv = qv + wave * 64 * EPT;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const uint32_t v = (uint32_t)slice_v(base, tid, q);
+      const bool s = (int)v < a.V && !(xv[q] <= xc) && v != vm;
+      const unsigned long long m = __ballot(s);
+      if (s) {
+        const int pos = n + (int)__popcll(m & below);
+        wx[pos] = xv[q];
+        wv[pos] = v;
+      }
+      n += (int)__popcll(m);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float by = NEG_INF;
+    uint32_t bv = 0xFFFFFFFFu;
+    for (int i = lane; i < n; i += 64) {
+      const float x = wx[i];
+      const uint32_t v = wv[i];
+      const float y = score_sampled(p, x, v);
+      const bool b = (y > by) || (y == by && v < bv);
+      by = b ? y : by;
+      bv = b ? v : bv;
+    }
+    const unsigned long long k = bv != 0xFFFFFFFFu ? make_key(by, bv) : 0ull;
+    const unsigned long long wk = wave_max_u64(k);
+    best = wk > best ? wk : best;
+  }
+  const unsigned long long gb = block_max_u64(best, red);
+  if (tid == 0) a.ckeys[(int64_t)row * a.nchunks + blockIdx.x] = gb;
+}
+
 // Launch 3: one wave per row reduces the candidate slots and the survivor pass's row key
 // to the token.
 __global__ void __launch_bounds__(256) gumbel_finish_kernel(SmpArgs a) {
@@ -502,19 +597,19 @@ __global__ void gumbel_scores_kernel(SmpArgs a) {
 using namespace vqk;
 
 static int64_t gumbel_nblk(int64_t V) { return (V + 1023) / 1024; }
-static int64_t gumbel_nchunks(int64_t V) { return (V + SMP_CHUNK - 1) / SMP_CHUNK; }
+static int64_t gumbel_nchunks(int64_t V, int64_t chunk) { return (V + chunk - 1) / chunk; }
 
 // ckeys [B, nchunks] u64, rkeys [B] u64, bkeys [B, nblk] u32: every launch writes each
 // value before reading it, so the workspace needs no initialisation.
 extern "C" int64_t vqk_gumbel_workspace_size(int64_t B, int64_t V) {
   if (B < 0 || V < 0) return 0;
-  return B * (gumbel_nchunks(V) + 1) * (int64_t)sizeof(unsigned long long) +
+  return B * (gumbel_nchunks(V, SMP_MIN_CHUNK) + 1) * (int64_t)sizeof(unsigned long long) +
          B * gumbel_nblk(V) * (int64_t)sizeof(uint32_t) + 16;
 }
 
 static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, const void* seeds) {
   if (!logits || B < 0 || V < 1 || ld < V) return VQK_EINVAL;
-  if (B > 65535 || V > (int64_t)INT32_MAX - SMP_CHUNK) return VQK_EUNSUPPORTED;
+  if (B > 65535 || V > (int64_t)INT32_MAX - SMP_THREADS * 64) return VQK_EUNSUPPORTED;
   if (!seeds) return VQK_EINVAL;
   return VQK_OK;
 }
@@ -541,19 +636,22 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   a.thr = topk_thr;
   a.out = out;
   a.nblk = (int)gumbel_nblk(V);
-  a.nchunks = (int)gumbel_nchunks(V);
+  // Small batches (up to ~2M logits) take the single-pass form: the whole call is then a
+  // few workgroup latencies long, and three launches would cost more than the extra
+  // scoring.  Larger ones take the candidate and survivor passes.
+  const bool small = B * V <= ((int64_t)2 << 20);
+  const int64_t max_chunks = gumbel_nchunks(V, SMP_MIN_CHUNK);
+  a.nchunks = (int)gumbel_nchunks(V, small ? SMP_THREADS * 4 : SMP_THREADS * 64);
   a.ckeys = (unsigned long long*)workspace;
-  a.rkeys = a.ckeys + B * (int64_t)a.nchunks;
+  a.rkeys = a.ckeys + B * max_chunks;
   a.bkeys = (uint32_t*)(a.rkeys + B);
   a.vec = (((uintptr_t)logits & 15) == 0 && (ld % 4) == 0) ? 1 : 0;
-  hipLaunchKernelGGL(gumbel_cand_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
-                     (hipStream_t)stream, a);
-  // survivor slices: 1024 logits per workgroup for small batches (more workgroups to spread
-  // a hot row over), 2048 beyond ~2M elements (measured best at B = 32 and 128)
-  if (B * V <= ((int64_t)2 << 20)) {
-    const int ns = (int)((V + SMP_THREADS * 4 - 1) / (SMP_THREADS * 4));
-    hipLaunchKernelGGL(gumbel_surv_kernel<4>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+  if (small) {
+    hipLaunchKernelGGL(gumbel_local_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+                       (hipStream_t)stream, a);
   } else {
+    hipLaunchKernelGGL(gumbel_cand_kernel<64>, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+                       (hipStream_t)stream, a);
     const int ns = (int)((V + SMP_THREADS * 8 - 1) / (SMP_THREADS * 8));
     hipLaunchKernelGGL(gumbel_surv_kernel<8>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
