@@ -928,6 +928,14 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
 template <int MODE, int NCT>
 static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, hipStream_t st) {
   // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
+#if VQK_LM_LDS_STAGES >= 6
+  // deeper rings (measured: no faster than 4 stages on MI355X, so not built by default)
+  if (stages == 8)
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 8>), dim3(grid), dim3(256), lds_bytes, st, a);
+  else if (stages == 6)
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 6>), dim3(grid), dim3(256), lds_bytes, st, a);
+  else
+#endif
   if (stages == 4)
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4>), dim3(grid), dim3(256), lds_bytes, st, a);
   else if (stages == 3)
@@ -986,7 +994,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   // The LDS-staged kernel needs whole 256-byte stages and 16-byte aligned scale rows; it
   // reserves 4 waves x 2 stages of ring next to the activations.
   const bool lds_path = VQK_LM_LDS && KB % 256 == 0 && ((uintptr_t)ws & 15) == 0;
-  const size_t ring2 = (size_t)4 * 2 * G::SLOT, ring4 = (size_t)4 * 4 * G::SLOT;
+  const size_t ring2 = (size_t)4 * 2 * G::SLOT;
   // batch group size: up to 16*NCT rows, limited by LDS
   int gmax = (int)(((lds_path ? lds_cap - ring2 : lds_cap) - 64) / xl.per_row());
   if (gmax < 1) return VQK_EUNSUPPORTED;
@@ -1031,10 +1039,9 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.lds_x_bytes = (int)lds;
     const int ntiles = (int)((M + 15) / 16);
     if (lds_path && lds + ring2 <= lds_cap) {
-      // the deepest ring (4, 3 or 2 stages per wave) that fits next to the activations
-      const size_t ring3 = (size_t)4 * 3 * G::SLOT;
-      const int stages = (VQK_LM_LDS_STAGES >= 4 && lds + ring4 <= lds_cap) ? 4
-                         : (VQK_LM_LDS_STAGES >= 3 && lds + ring3 <= lds_cap) ? 3 : 2;
+      // the deepest ring (8, 6, 4, 3 or 2 stages per wave) that fits next to the activations
+      auto fits = [&](int n) { return VQK_LM_LDS_STAGES >= n && lds + (size_t)4 * n * G::SLOT <= lds_cap; };
+      const int stages = fits(8) ? 8 : fits(6) ? 6 : fits(4) ? 4 : fits(3) ? 3 : 2;
       const size_t lds_l = lds + (size_t)4 * stages * G::SLOT;
       int per_cu_l = (int)(lds_cap / (lds_l + 512));
       if (per_cu_l > VQK_LM_LDS_WG_PER_CU) per_cu_l = VQK_LM_LDS_WG_PER_CU;
