@@ -162,6 +162,15 @@ int vqk_gemm_fp8(const uint8_t *w, const uint16_t *s_f16, const uint8_t *xq, uin
 int vqk_gemm_w8a8(const int8_t *w, const float *ws_f32, const int8_t *xq, float xs,
                   uint16_t *out_f16, int64_t ldo, int32_t *acc_i32, int64_t M, int64_t K,
                   int64_t B, vqk_stream_t stream);
+/* vqk_gemm_w8a8 with the per-tensor scale read from device memory (xs_dev: fp32 [1], as
+ * vqk_act_quant_int8 writes it), so no host synchronisation separates the activation
+ * quantization from the projection.  No counterpart in the reference, which passes
+ * x_scale.item() by value (src/vllm_quant_kernels/_quant.py:548); the lm_head wrapper uses
+ * it from batch 8 up, where quantizing the activations once per call beats doing it in
+ * every workgroup's prologue. */
+int vqk_gemm_w8a8_devscale(const int8_t *w, const float *ws_f32, const int8_t *xq,
+                           const float *xs_dev, uint16_t *out_f16, int64_t ldo, int32_t *acc_i32,
+                           int64_t M, int64_t K, int64_t B, vqk_stream_t stream);
 
 /* Pre-quantized-activation forms of the two MX GEMMs: xq e4m3 [B,K] (row stride K) and
  * xs E8M0 [B,K/32] come from the caller, as the reference's factory-built kernels take them.

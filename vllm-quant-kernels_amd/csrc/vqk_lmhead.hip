@@ -131,6 +131,7 @@ struct LmArgs {
   int M, K, Bg, Ball;
   int out_vec;          // 1 when 8-byte output stores are aligned
   float xs_val;         // W8A8 with pre-quantized activations: the per-tensor scale
+  const float* xs_dev;  //   ... or, when not null, where to read it (device memory)
   int lds_x_bytes;      // LDS bytes of the staged activations (fragments + MX scales), 16-aligned
   int xr;               // LDS bytes per batch row of fragments (16 * odd)
   int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
@@ -187,6 +188,7 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
     __syncthreads();
     xs_w8a8 = lds_red[16];
   } else if (MODE == M_W8A8) {
+    if (a.xs_dev) xs_w8a8 = *a.xs_dev;  // wave-uniform scalar read
     if (tid == 0) lds_red[16] = xs_w8a8;
   }
   const float xs_inv = 1.0f / xs_w8a8;  // W8A8: reciprocal for rint_div_i8 (IEEE division)
@@ -972,7 +974,7 @@ template <int MODE>
 static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xdt, int64_t ldx,
                          const uint8_t* xq, const uint8_t* xsq, uint16_t* out, int64_t ldo,
                          int32_t* acc, int64_t M, int64_t K, int64_t B, hipStream_t st,
-                         float xs_val = 0.f) {
+                         float xs_val = 0.f, const float* xs_dev = nullptr) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
   int rc = vqk_device_check();
@@ -1026,6 +1028,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.Ball = (int)B;
     a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
     a.xs_val = xs_val;
+    a.xs_dev = xs_dev;
     a.xr = xl.xr;
     if (xq) {
       a.xvec = ((uintptr_t)xq & 15) == 0 ? 1 : 0;  // rows are K bytes, K % 128 == 0
@@ -1152,4 +1155,12 @@ extern "C" int vqk_gemm_w8a8(const int8_t* w, const float* ws_f32, const int8_t*
   if (!xq) return VQK_EINVAL;
   return lmhead_launch<M_W8A8>((const uint8_t*)w, ws_f32, nullptr, VQK_F16, K, (const uint8_t*)xq, nullptr, out_f16,
                                ldo, acc_i32, M, K, B, (hipStream_t)stream, xs);
+}
+
+extern "C" int vqk_gemm_w8a8_devscale(const int8_t* w, const float* ws_f32, const int8_t* xq, const float* xs_dev,
+                                      uint16_t* out_f16, int64_t ldo, int32_t* acc_i32, int64_t M, int64_t K,
+                                      int64_t B, vqk_stream_t stream) {
+  if (!xq || !xs_dev) return VQK_EINVAL;
+  return lmhead_launch<M_W8A8>((const uint8_t*)w, ws_f32, nullptr, VQK_F16, K, (const uint8_t*)xq, nullptr, out_f16,
+                               ldo, acc_i32, M, K, B, (hipStream_t)stream, 0.f, xs_dev);
 }

@@ -73,54 +73,91 @@ __global__ void __launch_bounds__(QT) quant_rows_fp8_kernel(const void* w, int d
 template <int DT>
 __global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt, uint8_t* q,
                                 uint8_t* scales, int fp4, int vec) {
+  // Four lanes per 32-element group, 8 elements each: the group's amax takes two lane
+  // exchanges, then every lane encodes its own 8 elements (short per-lane chains: at
+  // activation sizes the launch is latency-bound).
   const int64_t G = K / 32;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= R * G) return;
-  const int64_t row = gid / G, grp = gid - row * G;
-  const int64_t off = row * ldt + grp * 32;
-  float v[32];
-  load_run<DT, 32>(t, off, vec != 0, v);
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t gid = tid >> 2;
+  const int part = (int)(tid & 3);
+  const bool live = gid < R * G;
+  const int64_t g = live ? gid : 0;  // idle lanes mirror group 0 so the exchanges see 4 lanes
+  const int64_t row = g / G, grp = g - row * G;
+  float v[8];
+  load_run<DT, 8>(t, row * ldt + grp * 32 + part * 8, vec != 0, v);
   float amax = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
   const int k = mx_exponent(amax, fp4 ? 6.0f : 448.0f);
   const float sc = exp2i(k);
-  scales[row * G + grp] = (uint8_t)(k + 127);
+  if (!live) return;
+  if (part == 0) scales[row * G + grp] = (uint8_t)(k + 127);
   if (!fp4) {
-    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t w[2] = {0, 0};
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      float y = fminf(fmaxf(v[e] / sc, -448.f), 448.f);
+    for (int e = 0; e < 8; ++e) {
+      const float y = fminf(fmaxf(v[e] / sc, -448.f), 448.f);
       w[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
     }
-    uint32_t* dst = (uint32_t*)(q + row * K + grp * 32);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = w[i];
+    uint32_t* dst = (uint32_t*)(q + row * K + grp * 32 + part * 8);
+    dst[0] = w[0];
+    dst[1] = w[1];
   } else {
-    uint32_t w[4] = {0, 0, 0, 0};
+    uint32_t w = 0;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) w[e >> 3] |= f32_to_e2m1(v[e] / sc) << (4 * (e & 7));
-    uint32_t* dst = (uint32_t*)(q + row * (K / 2) + grp * 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = w[i];
+    for (int e = 0; e < 8; ++e) w |= f32_to_e2m1(v[e] / sc) << (4 * e);
+    *(uint32_t*)(q + row * (K / 2) + grp * 16 + part * 4) = w;
   }
 }
 
-// Per-tensor INT8 activation quantization: a single workgroup (the activation is tiny).
-__global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int dt, int64_t ldx, int64_t B,
-                                                               int64_t K, int8_t* xq, float* xs) {
+// Per-tensor INT8 activation quantization: a single workgroup (the activation is tiny),
+// two passes (amax, then codes), 8 consecutive elements per thread and step when rows
+// allow 16-byte loads.  Codes are rint(x / s) exactly (rint_div_i8), clamped to +-127.
+template <int DT>
+__global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int64_t ldx, int64_t B,
+                                                               int64_t K, int vec, int8_t* xq, float* xs) {
   __shared__ float red[16];
+  const int64_t per_row = K / 8, total = B * per_row;
   float m = 0.f;
-  for (int64_t b = 0; b < B; ++b)
-    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load_as_f32(x, dt, b * ldx + k)));
+  if (vec) {
+#pragma unroll 4
+    for (int64_t c = threadIdx.x; c < total; c += blockDim.x) {
+      const int64_t b = c / per_row, k8 = c - b * per_row;
+      float v[8];
+      load_run<DT, 8>(x, b * ldx + 8 * k8, true, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+    }
+  } else {
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load_dt<DT>(x, b * ldx + k)));
+  }
   m = block_max(m, red);
   const float s = fmaxf(m / 127.0f, 1e-12f);
-  for (int64_t b = 0; b < B; ++b)
-    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
-      float v = __builtin_rintf(load_as_f32(x, dt, b * ldx + k) / s);
-      v = fminf(fmaxf(v, -127.f), 127.f);
-      xq[b * K + k] = (int8_t)(int)v;
+  const float r = 1.0f / s;
+  if (vec) {
+#pragma unroll 4
+    for (int64_t c = threadIdx.x; c < total; c += blockDim.x) {
+      const int64_t b = c / per_row, k8 = c - b * per_row;
+      float v[8];
+      load_run<DT, 8>(x, b * ldx + 8 * k8, true, v);
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = fminf(fmaxf(rint_div_i8(v[e], s, r), -127.f), 127.f);
+        w[e >> 2] |= ((uint32_t)(int)q & 0xFFu) << (8 * (e & 3));
+      }
+      *(uint2*)(xq + b * K + 8 * k8) = make_uint2(w[0], w[1]);
     }
+  } else {
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
+        const float q = fminf(fmaxf(rint_div_i8(load_dt<DT>(x, b * ldx + k), s, r), -127.f), 127.f);
+        xq[b * K + k] = (int8_t)(int)q;
+      }
+  }
   if (threadIdx.x == 0) *xs = s;
 }
 
@@ -173,7 +210,7 @@ static int quant_mx(const void* t, int dt, int64_t R, int64_t K, int64_t ldt, ui
   if (!t || !q || !s || !dt_ok(dt) || R < 0 || K < 1 || ldt < K) return VQK_EINVAL;
   if (K % 32 != 0) return VQK_EINVAL;
   if (R == 0) return VQK_OK;
-  const int64_t n = R * (K / 32);
+  const int64_t n = 4 * R * (K / 32);  // four lanes per 32-element group
   const int th = 256;
   const int64_t nb = (n + th - 1) / th;
   if (nb > INT32_MAX) return VQK_EUNSUPPORTED;
@@ -203,8 +240,15 @@ extern "C" int vqk_act_quant_int8(const void* x, int x_dtype, int64_t ldx, int64
   int rc = vqk_device_check();
   if (rc) return rc;
   if (!x || !xq || !xs || !dt_ok(x_dtype) || B < 0 || K < 1 || ldx < K) return VQK_EINVAL;
-  hipLaunchKernelGGL(act_quant_int8_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, x_dtype, ldx, B, K, xq,
-                     xs);
+  if (B == 0) return VQK_OK;
+  const int es = (x_dtype == VQK_F32) ? 4 : 2;
+  const int vec = (K % 8 == 0 && ((uintptr_t)x & 15) == 0 && (ldx * es) % 16 == 0 && ((uintptr_t)xq & 7) == 0) ? 1 : 0;
+  if (x_dtype == VQK_F32)
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F32>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
+  else if (x_dtype == VQK_F16)
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F16>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
+  else
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_BF16>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
   return finish();
 }
 

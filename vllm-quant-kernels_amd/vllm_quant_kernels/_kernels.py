@@ -148,7 +148,7 @@ def _x_for(x, K):
     return x
 
 
-# From this batch size on, the e4m3 / MX lm_head wrappers quantize the activations once in
+# From this batch size on, the W8A8, e4m3 and MX lm_head wrappers quantize the activations once in
 # a separate launch and run the pre-quantized kernel: the fused form re-quantizes the
 # activations in every workgroup's prologue, which costs more than a launch once the
 # batch is large (measured on MI355X at 248320 x 3072: ~12-18 us at B=16).
@@ -178,9 +178,12 @@ def lmhead_w8a8(x, w, ws, out=None, acc=None):
     M, K = w.shape
     x = _x_for(x, K)
     B = x.shape[0]
-    out = _out(out, B, M, x.device)
     if acc is not None:
         assert acc.dtype == torch.int32 and acc.shape == (B, M) and acc.is_contiguous()
+    if B >= SEPARATE_ACT_QUANT_MIN_B:
+        xq, xs = act_quant_int8(x)
+        return gemm_w8a8_devscale(xq, xs, w, ws, out=out, acc=acc)
+    out = _out(out, B, M, x.device)
     _lib.call("vqk_lmhead_w8a8", w.data_ptr(), ws.data_ptr(), x.data_ptr(), _DT[x.dtype], x.stride(0),
               out.data_ptr(), out.stride(0), acc.data_ptr() if acc is not None else None, M, K, B,
               _stream(x))
@@ -257,6 +260,20 @@ def gemm_w8a8(xq, xs: float, w, ws, out=None, acc=None):
     out = _out(out, B, M, xq.device)
     _lib.call("vqk_gemm_w8a8", w.data_ptr(), ws.data_ptr(), xq.data_ptr(), float(xs), out.data_ptr(),
               out.stride(0), acc.data_ptr() if acc is not None else None, M, K, B, _stream(xq))
+    return out
+
+
+def gemm_w8a8_devscale(xq, xs, w, ws, out=None, acc=None):
+    """gemm_w8a8 with the per-tensor scale xs (fp32 [1]) read on the device: no host sync."""
+    _dev(xq, xs, w, ws, acc)
+    M, K = w.shape
+    B = xq.shape[0]
+    xq = xq.contiguous()
+    assert xs.dtype == torch.float32 and xs.numel() == 1
+    out = _out(out, B, M, xq.device)
+    _lib.call("vqk_gemm_w8a8_devscale", w.data_ptr(), ws.data_ptr(), xq.data_ptr(), xs.data_ptr(),
+              out.data_ptr(), out.stride(0), acc.data_ptr() if acc is not None else None, M, K, B,
+              _stream(xq))
     return out
 
 
