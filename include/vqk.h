@@ -206,6 +206,28 @@ int vqk_gumbel_argmax(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *topk_thr, int64_t *out, void *workspace,
                       int64_t ws_bytes, vqk_stream_t stream);
 
+/* Fused lm_head + Gumbel-argmax sampling (opt-in; one batch group of B <= 32 rows).
+ * Runs the `mode` projection exactly as vqk_lmhead_<mode> does (same arguments: w, ws,
+ * x, x_dtype, ldx, out_f16, ldo, M, K, B; for VQK_MODE_MXFP4, w is the packed [M,K/2] form
+ * and K the logical K; W8A16 takes fp16 x only) and, in the same launch's epilogue,
+ * scores every stored logit as vqk_gumbel_argmax does with the fp32 value of the fp16
+ * logit: y = fp32(out[b,m]), greedy rows (temp NULL or T[b] < 1e-5) take y, the others
+ * y / T[b] + G(seed_b, m).  A second, tiny launch reduces the per-wave best keys to
+ * tokens[b] (int64 [B]).  The tokens equal those of vqk_lmhead_<mode> followed by
+ * vqk_gumbel_argmax on the fp32-converted logits, bit for bit; the logits are still
+ * written to out_f16.  No top-k (its threshold depends on the finished logits).
+ *   workspace: >= vqk_lmhead_sample_workspace_size(B) bytes, 8-byte aligned, no
+ *   initialisation needed.
+ * Replaces: _quantized_forward (src/vllm_quant_kernels/_quant.py:382-397) followed by
+ *           FusedSampler.sample's fast path (src/vllm_quant_kernels/_sampler.py:144-206);
+ *           the reference runs them as separate launches with the logits in between. */
+enum { VQK_MODE_W8A16 = 0, VQK_MODE_W8A8 = 1, VQK_MODE_FP8 = 2, VQK_MODE_MXFP8 = 3, VQK_MODE_MXFP4 = 4 };
+int64_t vqk_lmhead_sample_workspace_size(int64_t B);
+int vqk_lmhead_sample(int mode, const void *w, const void *ws, const void *x, int x_dtype,
+                      int64_t ldx, uint16_t *out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B,
+                      const float *temp, const void *seeds, int seed_is_64bit, int64_t *tokens,
+                      void *workspace, int64_t ws_bytes, vqk_stream_t stream);
+
 /* Debug form of the sampler arithmetic: writes y (the value the argmax is taken over,
  * -inf where masked) for every element to scores [B,V] (row stride V).  Same arguments
  * as vqk_gumbel_argmax minus the workspace.  Used by the parity tests to compare the

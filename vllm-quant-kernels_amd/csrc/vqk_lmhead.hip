@@ -137,7 +137,39 @@ struct LmArgs {
   int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
   int xs_off;           // MX: LDS byte offset of the activation scales
   int xvec;             // 1 when activation rows (x or xq) allow 16-byte loads
+  // fused Gumbel-argmax epilogue (the sampling form only)
+  const float* stemp;   // [Bg] temperatures or null (greedy)
+  const void* sseeds;   // [Bg] int32 or int64 seeds
+  int sseed64;
+  unsigned long long* skeys;  // [Bg, waves of the launch] best key of each wave and row
 };
+
+// Per-lane state of the fused sampling epilogue: lane (g, j) sees batch row ct*16 + j of
+// every column tile ct; its running best key over the rows it has scored, and that batch
+// row's sampling parameters.
+template <int NCT>
+struct SmpLane {
+  unsigned long long best[NCT];
+  float T[NCT];
+  uint32_t k0[NCT], k1[NCT];
+  bool greedy[NCT];
+};
+template <int NCT>
+__device__ __forceinline__ void smp_lane_init(const LmArgs& a, int lane, SmpLane<NCT>& sl) {
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int b = min(ct * 16 + (lane & 15), a.Bg - 1);
+    sl.best[ct] = 0ull;
+    const float t = a.stemp ? a.stemp[b] : 0.f;
+    sl.greedy[ct] = !a.stemp || t < 1e-5f;
+    sl.T[ct] = t;
+    uint64_t sd;
+    if (a.sseed64) sd = ((const uint64_t*)a.sseeds)[b];
+    else sd = (uint64_t)(int64_t)((const int32_t*)a.sseeds)[b];
+    sl.k0[ct] = (uint32_t)sd;
+    sl.k1[ct] = (uint32_t)(sd >> 32);
+  }
+}
 
 
 // ---------------------------------------------------------------------------------------
@@ -542,7 +574,7 @@ __device__ __forceinline__ void row_scales(const LmArgs& a, int m0, int lane, fl
 
 template <int MODE, int NCT>
 __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, int m0, int lane,
-                                         float xs_w8a8, const float (&sc)[4]) {
+                                         float xs_w8a8, const float (&sc)[4], SmpLane<NCT>* sl = nullptr) {
   const int g = lane >> 4, j = lane & 15;
   const int mr = m0 + 4 * g;
   const bool full = (mr + 3 < a.M);
@@ -562,6 +594,25 @@ __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, i
           r = acc.v[ct][e];
         }
         o[e] = f2h(r);
+      }
+      if (sl) {
+        // Sampling epilogue: the score of each stored logit exactly as the stand-alone
+        // sampler computes it from the fp16 logits converted to fp32 (y = fp32(fp16(r)),
+        // then y / T + G(seed_b, m)), folded into the lane's running best key.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = mr + e;
+          if (m < a.M) {
+            const float y = h2f(o[e]);
+            float sy = y;
+            if (!sl->greedy[ct]) {
+              const float q = y / sl->T[ct];
+              sy = q + gumbel_from_uniform(philox_uniform(philox_word0_vk((uint32_t)m, sl->k0[ct], sl->k1[ct])));
+            }
+            const unsigned long long k = make_key(sy, (uint32_t)m);
+            sl->best[ct] = k > sl->best[ct] ? k : sl->best[ct];
+          }
+        }
       }
       uint16_t* op = a.out + (int64_t)b * a.ldo + mr;
       if (full && a.out_vec) {
@@ -773,7 +824,7 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
   }
 }
 
-template <int MODE, int NCT, int S>
+template <int MODE, int NCT, int S, bool SMP = false>
 __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
@@ -794,7 +845,10 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
   const int ntiles = (a.M + 15) >> 4;
   const int wid = blockIdx.x * 4 + wave;
   const int total = gridDim.x * 4;
-  if (wid >= ntiles) return;
+  if (wid >= ntiles) {
+    if (SMP && (threadIdx.x & 63) < (unsigned)a.Bg) a.skeys[(int64_t)(threadIdx.x & 63) * total + wid] = 0ull;
+    return;
+  }
   const int my_tiles = (ntiles - 1 - wid) / total + 1;
   const int SPT = KB >> 8;  // stages per tile (KB % 256 == 0, host guarantees)
   const int nst = my_tiles * SPT;
@@ -830,6 +884,8 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
   Acc<MODE, NCT> acc;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
+  SmpLane<NCT> sl;
+  if constexpr (SMP) smp_lane_init<NCT>(a, lane, sl);
   uint32_t sdw[16];  // the tile's row-scale dwords (wave-uniform), fetched at its first stage
   int ctile = wid, cks = 0;
 
@@ -865,6 +921,14 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
           }
           compute_chunk<MODE, NCT>(acc, st, 2 * cks + cc, g, xp);
         }
+        // Refill the slot before any epilogue work, so the stream keeps S stages in flight
+        // while a tile's results are scaled, stored (and, in the sampling form, scored).
+        // The slot's ds_reads have completed before the DMA may overwrite it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (iq < nst) {
+          issue_stage<MODE>(a, KB, itile, iks, ring + so, lane, io);
+          advance_issue();
+        }
         if (cks == SPT - 1) {
           float tsc[4];
           if (!T::ROWSCALE) {
@@ -876,22 +940,49 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
           } else {
             row_scales<MODE>(a, ctile * 16, lane, tsc);  // the ragged last tile
           }
-          epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc);
+          epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, SMP ? &sl : nullptr);
         }
         if (++cks == SPT) {
           cks = 0;
           ctile += total;
         }
-        // the slot's ds_reads have completed before the DMA refill may overwrite it
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (iq < nst) {
-          issue_stage<MODE>(a, KB, itile, iks, ring + so, lane, io);
-          advance_issue();
-        }
       }
     }
   }
   wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
+  if constexpr (SMP) {
+    // the wave's best key of each batch row: lanes j, j+16, j+32, j+48 hold row j's
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      unsigned long long k = sl.best[ct];
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const unsigned long long o = __shfl_xor(k, off);
+        k = o > k ? o : k;
+      }
+      const int b = ct * 16 + lane;
+      if (lane < 16 && b < a.Bg) a.skeys[(int64_t)b * total + wid] = k;
+    }
+  }
+}
+
+// The token of each batch row of a fused lm_head + sampling launch: one wave per row
+// reduces the row's per-wave keys.
+__global__ void __launch_bounds__(256) lmhead_sample_finish_kernel(const unsigned long long* skeys, int nslot,
+                                                                   int B, int64_t* tokens) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= B) return;
+  unsigned long long k = 0ull;
+  for (int i = lane; i < nslot; i += 64) {
+    const unsigned long long o = skeys[(int64_t)row * nslot + i];
+    k = o > k ? o : k;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(k, off);
+    k = o > k ? o : k;
+  }
+  if (lane == 0) tokens[row] = (int64_t)(~(uint32_t)(k & 0xFFFFFFFFull));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -927,26 +1018,37 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
   return e == hipSuccess ? VQK_OK : (int)e;
 }
 
-template <int MODE, int NCT>
+template <int MODE, int NCT, bool SMP = false>
 static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, hipStream_t st) {
   // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
 #if VQK_LM_LDS_STAGES >= 6
   // deeper rings (measured: no faster than 4 stages on MI355X, so not built by default)
   if (stages == 8)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 8>), dim3(grid), dim3(256), lds_bytes, st, a);
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 8, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else if (stages == 6)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 6>), dim3(grid), dim3(256), lds_bytes, st, a);
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 6, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else
 #endif
   if (stages == 4)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4>), dim3(grid), dim3(256), lds_bytes, st, a);
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else if (stages == 3)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 3>), dim3(grid), dim3(256), lds_bytes, st, a);
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 3, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 2>), dim3(grid), dim3(256), lds_bytes, st, a);
+    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 2, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }
+
+// The fused sampling form's extra arguments.
+struct SmpCall {
+  const float* temp;
+  const void* seeds;
+  int seed64;
+  int64_t* tokens;
+  unsigned long long* skeys;
+  int64_t slots_per_row;  // capacity of skeys per batch row
+};
+constexpr int64_t LM_SMP_SLOTS = 4096;  // per batch row: 4 waves x up to 1024 workgroups
 
 // LDS layout of the staged activations (see stage_x_dt): fragment rows of xr bytes with
 // xr/16 odd, then for MX modes scale rows of xsr dwords with xsr odd.
@@ -974,7 +1076,7 @@ template <int MODE>
 static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xdt, int64_t ldx,
                          const uint8_t* xq, const uint8_t* xsq, uint16_t* out, int64_t ldo,
                          int32_t* acc, int64_t M, int64_t K, int64_t B, hipStream_t st,
-                         float xs_val = 0.f, const float* xs_dev = nullptr) {
+                         float xs_val = 0.f, const float* xs_dev = nullptr, const SmpCall* smp = nullptr) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
   int rc = vqk_device_check();
@@ -1004,6 +1106,8 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   if (gmax > 16 * nct_max) gmax = 16 * nct_max;
   const int ngroups = (int)((B + gmax - 1) / gmax);
   const int gsize = (int)((B + ngroups - 1) / ngroups);  // balanced groups
+  // the fused sampling form runs one batch group through the LDS kernel
+  if (smp && (ngroups != 1 || !lds_path)) return VQK_EUNSUPPORTED;
   const int ncu = vqk_cu_count();
   const int threads = 512;
 
@@ -1029,6 +1133,10 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
     a.xs_val = xs_val;
     a.xs_dev = xs_dev;
+    a.stemp = smp ? smp->temp : nullptr;
+    a.sseeds = smp ? smp->seeds : nullptr;
+    a.sseed64 = smp ? smp->seed64 : 0;
+    a.skeys = smp ? smp->skeys : nullptr;
     a.xr = xl.xr;
     if (xq) {
       a.xvec = ((uintptr_t)xq & 15) == 0 ? 1 : 0;  // rows are K bytes, K % 128 == 0
@@ -1060,6 +1168,21 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       }
       const int nct_l = (Bg + 15) / 16;
       int rcl;
+      if (smp) {
+        if (4 * (int64_t)grid_l > smp->slots_per_row) return VQK_EWORKSPACE;
+        if constexpr (MODE == M_W8A16) {
+          rcl = launch_lds<MODE, 1, true>(a, stages, lds_l, grid_l, st);
+        } else {
+          rcl = (nct_l == 1) ? launch_lds<MODE, 1, true>(a, stages, lds_l, grid_l, st)
+                             : launch_lds<MODE, 2, true>(a, stages, lds_l, grid_l, st);
+        }
+        if (rcl) return rcl;
+        hipLaunchKernelGGL(lmhead_sample_finish_kernel, dim3((unsigned)((Bg + 3) / 4)), dim3(256), 0, st,
+                           smp->skeys, 4 * grid_l, Bg, smp->tokens);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+        continue;
+      }
       if constexpr (MODE == M_W8A16) {
         rcl = launch_lds<MODE, 1>(a, stages, lds_l, grid_l, st);
       } else {
@@ -1069,6 +1192,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       if (rcl) return rcl;
       continue;
     }
+    if (smp) return VQK_EUNSUPPORTED;  // the sampling form needs the LDS kernel
     int per_cu = (int)((150 * 1024) / (lds + 1024));
     if (per_cu > VQK_LM_WG_PER_CU) per_cu = VQK_LM_WG_PER_CU;
     if (per_cu < 1) per_cu = 1;
@@ -1163,4 +1287,47 @@ extern "C" int vqk_gemm_w8a8_devscale(const int8_t* w, const float* ws_f32, cons
   if (!xq || !xs_dev) return VQK_EINVAL;
   return lmhead_launch<M_W8A8>((const uint8_t*)w, ws_f32, nullptr, VQK_F16, K, (const uint8_t*)xq, nullptr, out_f16,
                                ldo, acc_i32, M, K, B, (hipStream_t)stream, 0.f, xs_dev);
+}
+
+extern "C" int64_t vqk_lmhead_sample_workspace_size(int64_t B) {
+  return B < 0 ? 0 : B * LM_SMP_SLOTS * (int64_t)sizeof(unsigned long long);
+}
+
+extern "C" int vqk_lmhead_sample(int mode, const void* w, const void* ws, const void* x, int x_dtype, int64_t ldx,
+                                 uint16_t* out_f16, int64_t ldo, int64_t M, int64_t K, int64_t B, const float* temp,
+                                 const void* seeds, int seed_is_64bit, int64_t* tokens, void* workspace,
+                                 int64_t ws_bytes, vqk_stream_t stream) {
+  if (!x || !seeds || !tokens || !workspace) return VQK_EINVAL;
+  if (B > 32 || M > (int64_t)UINT32_MAX / 2) return VQK_EUNSUPPORTED;
+  if (ws_bytes < vqk_lmhead_sample_workspace_size(B)) return VQK_EWORKSPACE;
+  if (((uintptr_t)workspace & 7) != 0) return VQK_EINVAL;
+  SmpCall sc;
+  sc.temp = temp;
+  sc.seeds = seeds;
+  sc.seed64 = seed_is_64bit ? 1 : 0;
+  sc.tokens = tokens;
+  sc.skeys = (unsigned long long*)workspace;
+  sc.slots_per_row = LM_SMP_SLOTS;
+  const hipStream_t st = (hipStream_t)stream;
+  const uint8_t* wb = (const uint8_t*)w;
+  switch (mode) {
+    case VQK_MODE_W8A16:
+      if (x_dtype != VQK_F16) return VQK_EINVAL;
+      return lmhead_launch<M_W8A16>(wb, ws, x, VQK_F16, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B, st,
+                                    0.f, nullptr, &sc);
+    case VQK_MODE_W8A8:
+      return lmhead_launch<M_W8A8>(wb, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B, st,
+                                   0.f, nullptr, &sc);
+    case VQK_MODE_FP8:
+      return lmhead_launch<M_FP8>(wb, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B, st,
+                                  0.f, nullptr, &sc);
+    case VQK_MODE_MXFP8:
+      return lmhead_launch<M_MXFP8>(wb, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B, st,
+                                    0.f, nullptr, &sc);
+    case VQK_MODE_MXFP4:
+      return lmhead_launch<M_MXFP4>(wb, ws, x, x_dtype, ldx, nullptr, nullptr, out_f16, ldo, nullptr, M, K, B, st,
+                                    0.f, nullptr, &sc);
+    default:
+      return VQK_EINVAL;
+  }
 }

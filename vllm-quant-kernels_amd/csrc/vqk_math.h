@@ -214,6 +214,25 @@ __device__ __forceinline__ uint32_t philox_word0(uint32_t v, uint32_t k0, uint32
   return c0;
 }
 
+// philox_word0 for a key that differs between lanes (plain xors, no uniform operand).
+__device__ __forceinline__ uint32_t philox_word0_vk(uint32_t v, uint32_t k0, uint32_t k1) {
+  uint32_t c0 = v, c1 = 0u, c2 = 0u, c3 = 0u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t pa = (uint64_t)PHILOX_MA * c0;
+    const uint64_t pb = (uint64_t)PHILOX_MB * c2;
+    const uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
+    c0 = n0;
+    c2 = n2;
+    k0 += PHILOX_WA;
+    k1 += PHILOX_WB;
+  }
+  return c0;
+}
+
 // Triton's uint_to_uniform_float for a 32-bit word: reinterpret as int32, fold negatives
 // with -x-1, convert to float (RNE) and multiply by float(4.6566127342e-10) = 0x2FFFFFFF.
 __device__ __forceinline__ float philox_uniform(uint32_t w) {
@@ -277,6 +296,11 @@ __device__ __forceinline__ uint32_t orderable(float y) {
 __device__ __forceinline__ float from_orderable(uint32_t k) {
   uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
   return __uint_as_float(b);
+}
+
+// Argmax key of score y at vocabulary index v: larger y first, then smaller v.
+__device__ __forceinline__ unsigned long long make_key(float y, uint32_t v) {
+  return ((unsigned long long)orderable(y) << 32) | (unsigned long long)(~v);
 }
 
 }  // namespace vqk

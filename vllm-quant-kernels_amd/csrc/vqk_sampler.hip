@@ -108,9 +108,6 @@ __device__ __forceinline__ float score_sampled(const RowParams& p, float x, uint
   return a + gumbel_from_uniform(philox_uniform(philox_word0(v, p.k0, p.k1)));
 }
 
-__device__ __forceinline__ unsigned long long make_key(float y, uint32_t v) {
-  return ((unsigned long long)orderable(y) << 32) | (unsigned long long)(~v);
-}
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
 #pragma unroll

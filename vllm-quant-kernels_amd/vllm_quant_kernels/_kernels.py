@@ -241,6 +241,40 @@ def lmhead_mxfp4(x, w_packed, ws, K=None, out=None):
     return out
 
 
+
+_SAMPLE_MODES = {"w8a16": 0, "w8a8": 1, "fp8": 2, "mxfp8": 3, "mxfp4": 4}
+
+
+def lmhead_sample(mode: str, x, w, ws, temperature, seeds, K=None, out=None):
+    """Fused lm_head + Gumbel-argmax sampling (opt-in, B <= 32): returns (tokens int64 [B],
+    logits fp16 [B,M]).  The tokens equal those of lmhead_<mode> followed by
+    fused_gumbel_sample(logits.float(), temperature, seeds) bit for bit; the sampling runs
+    in the projection's epilogue, so the logits are not re-read.  No top-k."""
+    code = _SAMPLE_MODES[mode]
+    _dev(x, w, ws, seeds)
+    _contig(w, "w")
+    M = w.shape[0]
+    K = int(K) if K is not None else (2 * w.shape[1] if mode == "mxfp4" else w.shape[1])
+    x = _x_for(x, K)
+    if mode == "w8a16" and x.dtype != torch.float16:
+        x = x.to(torch.float16)
+    B = x.shape[0]
+    assert seeds.shape == (B,) and seeds.dtype in (torch.int32, torch.int64)
+    seeds = seeds.contiguous()
+    if temperature is not None:
+        assert temperature.shape == (B,) and temperature.dtype == torch.float32
+        temperature = temperature.contiguous()
+    out = _out(out, B, M, x.device)
+    tokens = torch.empty(B, dtype=torch.int64, device=x.device)
+    need = int(_lib.load().vqk_lmhead_sample_workspace_size(B))
+    wsp = torch.empty(max(need, 8), dtype=torch.uint8, device=x.device)
+    _lib.call("vqk_lmhead_sample", code, w.data_ptr(), ws.data_ptr(), x.data_ptr(), _DT[x.dtype], x.stride(0),
+              out.data_ptr(), out.stride(0), M, K, B,
+              temperature.data_ptr() if temperature is not None else None,
+              seeds.data_ptr(), 1 if seeds.dtype == torch.int64 else 0, tokens.data_ptr(),
+              wsp.data_ptr(), wsp.numel(), _stream(x))
+    return tokens, out
+
 def gemm_fp8(xq, w, s, out=None):
     _dev(xq, w, s)
     M, K = w.shape
