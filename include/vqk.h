@@ -228,6 +228,21 @@ int vqk_lmhead_sample(int mode, const void *w, const void *ws, const void *x, in
                       const float *temp, const void *seeds, int seed_is_64bit, int64_t *tokens,
                       void *workspace, int64_t ws_bytes, vqk_stream_t stream);
 
+/* Per-row top-k threshold on the device: thr[b] = the max(top_k[b], 1)-th largest raw
+ * logit of row b (NaN ranked largest), or -inf for every row when max_b top_k[b] >= V
+ * (the reference's "all rows disabled" case, where it passes no threshold; -inf masks
+ * nothing).  Feeds vqk_gumbel_argmax's topk_thr with no host synchronisation.
+ *   top_k    int32 [B] (top_k_is_64bit = 0) or int64 [B] (= 1), device memory.
+ *   thr      fp32 [B].
+ *   workspace: >= vqk_topk_threshold_workspace_size(B, V) bytes, 4-byte aligned, no
+ *   initialisation needed.  Two launches.
+ * Replaces: _compute_topk_threshold (src/vllm_quant_kernels/_sampler.py:62-93):
+ *           top_k.max().item(), torch.topk and gather. */
+int64_t vqk_topk_threshold_workspace_size(int64_t B, int64_t V);
+int vqk_topk_threshold(const float *logits, int64_t ld, int64_t B, int64_t V, const void *top_k,
+                       int top_k_is_64bit, float *thr, void *workspace, int64_t ws_bytes,
+                       vqk_stream_t stream);
+
 /* Debug form of the sampler arithmetic: writes y (the value the argmax is taken over,
  * -inf where masked) for every element to scores [B,V] (row stride V).  Same arguments
  * as vqk_gumbel_argmax minus the workspace.  Used by the parity tests to compare the

@@ -19,7 +19,7 @@ REPO = os.path.dirname(os.path.dirname(HERE))
 INCLUDE = os.path.join(REPO, "include")
 DEFAULT_OUT = os.path.join(PKG, "libvqk_hip.so")
 
-SOURCES = ["vqk_device.hip", "vqk_quant.hip", "vqk_lmhead.hip", "vqk_sampler.hip"]
+SOURCES = ["vqk_device.hip", "vqk_quant.hip", "vqk_lmhead.hip", "vqk_sampler.hip", "vqk_topk.hip"]
 
 
 def hipcc():

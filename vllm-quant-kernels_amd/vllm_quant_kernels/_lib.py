@@ -50,6 +50,8 @@ SIGNATURES = {
     "vqk_gemm_w8a8": (_I, [_P, _P, _P, ctypes.c_float, _P, _L, _P, _L, _L, _L, _P]),
     "vqk_gemm_w8a8_devscale": (_I, [_P, _P, _P, _P, _P, _L, _P, _L, _L, _L, _P]),
     "vqk_lmhead_sample_workspace_size": (_L, [_L]),
+    "vqk_topk_threshold_workspace_size": (_L, [_L, _L]),
+    "vqk_topk_threshold": (_I, [_P, _L, _L, _L, _P, _I, _P, _P, _L, _P]),
     "vqk_lmhead_sample": (_I, [_I, _P, _P, _P, _I, _L, _P, _L, _L, _L, _L, _P, _P, _I, _P, _P, _L, _P]),
     "vqk_gemm_mxfp8": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _L, _P]),
     "vqk_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _L, _P]),

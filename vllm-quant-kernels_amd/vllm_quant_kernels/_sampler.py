@@ -14,7 +14,7 @@ from typing import TYPE_CHECKING
 
 import torch
 
-from ._sampler_kernels import fused_gumbel_sample
+from ._sampler_kernels import fused_gumbel_sample, topk_threshold
 
 if TYPE_CHECKING:  # pragma: no cover
     from vllm.v1.sample.metadata import SamplingMetadata
@@ -87,7 +87,8 @@ def install_fused_sampler() -> None:
             B, V = logits.shape
             thr = None
             if sm.top_k is not None:
-                thr = _compute_topk_threshold(logits, sm.top_k, V)
+                # on the device, no host sync; equal in effect to _compute_topk_threshold
+                thr = topk_threshold(logits, sm.top_k)
             seeds = _make_seeds(B, logits.device)
             sampled = fused_gumbel_sample(
                 logits=logits,

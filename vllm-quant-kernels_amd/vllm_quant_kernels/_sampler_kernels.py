@@ -99,3 +99,26 @@ def gumbel_scores(logits, temperature, seeds, topk_threshold=None) -> torch.Tens
         scores.data_ptr(), stream,
     )
     return scores
+
+
+def topk_threshold(logits: torch.Tensor, top_k: torch.Tensor) -> torch.Tensor:
+    """Per-row top-k threshold computed on the device (two short launches, no host sync):
+    thr[b] = the max(top_k[b], 1)-th largest raw logit of row b, or -inf for every row
+    when max(top_k) >= V, where the reference returns None (-inf masks nothing, so the
+    sampler's result is the same).  Replaces the reference's _compute_topk_threshold
+    (src/vllm_quant_kernels/_sampler.py:62-93: .item(), torch.topk, gather)."""
+    B, V = logits.shape
+    assert logits.dtype == torch.float32 and logits.is_contiguous()
+    assert top_k.shape == (B,) and top_k.dtype in (torch.int32, torch.int64)
+    if not logits.is_cuda:
+        raise ValueError("topk_threshold: logits must live on the ROCm device")
+    top_k = top_k.to(logits.device).contiguous()
+    thr = torch.empty(B, dtype=torch.float32, device=logits.device)
+    if B == 0:
+        return thr
+    need = int(_lib.load().vqk_topk_threshold_workspace_size(B, V))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=logits.device)
+    _lib.call("vqk_topk_threshold", logits.data_ptr(), logits.stride(0), B, V, top_k.data_ptr(),
+              1 if top_k.dtype == torch.int64 else 0, thr.data_ptr(), ws.data_ptr(), ws.numel(),
+              torch.cuda.current_stream(logits.device).cuda_stream)
+    return thr
