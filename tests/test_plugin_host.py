@@ -11,6 +11,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 from types import SimpleNamespace
 
 import pytest
@@ -324,3 +325,81 @@ def test_library_has_gfx950_code_only():
     from vllm_quant_kernels import _lib
     targets = [t for t in _bundle_targets(_lib.LIB_PATH) if "amdgcn" in t]
     assert targets and all(t.endswith("gfx950") for t in targets), targets
+
+
+# ---------------------------------------------------------------------------------------
+# on-disk quantized lm_head (safetensors)
+
+def _fake_head(M, K, seed=0):
+    from types import SimpleNamespace
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(M, K, generator=g).half()
+    return SimpleNamespace(weight=SimpleNamespace(data=w, dtype=w.dtype, shape=w.shape, device=w.device)), g
+
+
+@pytest.mark.parametrize("mode", ["int8", "w8a8", "fp8", "mxfp8", "mxfp4"])
+def test_quantized_checkpoint_round_trip(tmp_path, mode):
+    from vllm_quant_kernels import _checkpoint as C
+    M, K = 300, 128
+    head, g = _fake_head(M, K)
+    kb = K // 2 if mode == "mxfp4" else K
+    wname, sname = C.MODE_TENSORS[mode]
+    wt = C._DTYPES[wname]
+    q = torch.randint(-128 if wt == torch.int8 else 0, 128 if wt == torch.int8 else 256, (M, kb),
+                      generator=g, dtype=torch.int32).to(wt)
+    st = C._DTYPES[sname]
+    s = (torch.randint(100, 150, (M, K // 32), generator=g, dtype=torch.int32).to(st) if mode.startswith("mx")
+         else torch.rand(M, generator=g).to(st))
+    setattr(head, wname, q)
+    setattr(head, sname, s)
+    path = str(tmp_path / "lm.safetensors")
+    assert C.save_quantized(head, path) == mode
+    fresh, _ = _fake_head(M, K)                       # same weight (same seed)
+    assert C.load_quantized(fresh, path) == mode
+    assert torch.equal(getattr(fresh, wname), q) and torch.equal(getattr(fresh, sname), s)
+    if mode == "mxfp4":
+        assert fresh._mxfp4_K == K
+    other, _ = _fake_head(M, K, seed=1)               # another weight: refused
+    assert C.load_quantized(other, path) is None and not hasattr(other, wname)
+    wrong = "int8" if mode != "int8" else "fp8"
+    assert C.load_quantized(fresh, path, mode=wrong) is None
+    assert C.load_quantized(fresh, str(tmp_path / "missing.safetensors")) is None
+
+
+def test_quantized_checkpoint_rejects_foreign_files(tmp_path):
+    from safetensors.torch import save_file
+    from vllm_quant_kernels import _checkpoint as C
+    head, _ = _fake_head(64, 32)
+    p = str(tmp_path / "x.safetensors")
+    save_file({"int8_w": torch.zeros(64, 32, dtype=torch.int8)}, p, metadata={"format": "other"})
+    assert C.load_quantized(head, p) is None
+    meta = {"format": C.FORMAT, "version": C.VERSION, "mode": "int8", "M": "64", "K": "32",
+            "source_dtype": "float16", "fingerprint": C.fingerprint(head.weight.data)}
+    save_file({"int8_w": torch.zeros(64, 32, dtype=torch.uint8),              # wrong dtype
+               "int8_scales": torch.zeros(64, dtype=torch.float16)}, p, metadata=meta)
+    assert C.load_quantized(head, p) is None
+    save_file({"int8_w": torch.zeros(64, 16, dtype=torch.int8),               # wrong shape
+               "int8_scales": torch.zeros(64, dtype=torch.float16)}, p, metadata=meta)
+    assert C.load_quantized(head, p) is None
+
+
+def test_init_cached_writes_then_loads(tmp_path, monkeypatch, capsys):
+    from vllm_quant_kernels._quant import QuantizedLogitsProcessor
+    M, K = 200, 64
+    head, _ = _fake_head(M, K)
+    monkeypatch.setenv("VQK_LMHEAD_CACHE_DIR", str(tmp_path))
+    calls = []
+
+    def quantize():
+        calls.append(1)
+        head._w8a8_w = torch.ones(M, K, dtype=torch.int8)
+        head._w8a8_scales = torch.full((M,), 0.5)
+
+    proc = QuantizedLogitsProcessor.__new__(QuantizedLogitsProcessor)
+    proc._init_cached("w8a8", head, head.weight.data, sys, quantize)
+    assert calls == [1] and (tmp_path / f"lm_head_w8a8_{M}x{K}.safetensors").exists()
+    head2, _ = _fake_head(M, K)
+    proc._init_cached("w8a8", head2, head2.weight.data, sys, quantize)
+    assert calls == [1]                                # loaded, not re-quantized
+    assert torch.equal(head2._w8a8_w, head._w8a8_w) and hasattr(head2, "_w8a8_gemm_kernel")
+    assert "loaded from" in capsys.readouterr().err

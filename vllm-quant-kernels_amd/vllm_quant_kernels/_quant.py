@@ -26,6 +26,7 @@ from typing import Optional
 import torch
 
 from . import _kernels as K_
+from . import _checkpoint as _ckpt
 from . import _lib
 from ._kernels import MXFP4_GROUP_SIZE, MXFP8_GROUP_SIZE  # noqa: F401  (reference re-export)
 
@@ -156,7 +157,7 @@ class QuantizedLogitsProcessor(LogitsProcessor):
                 print(f"{_TAG} VLLM_USE_MXFP4_LMHEAD: the gfx950 kernel needs K % 256 == 0 "
                       f"(got K={Kdim}), falling back to int8", file=_sys.stderr, flush=True)
             else:
-                self._init_mxfp4(lm_head, w, _sys)
+                self._init_cached("mxfp4", lm_head, w, _sys, lambda: self._init_mxfp4(lm_head, w, _sys))
                 return
 
         if _env_bool("VLLM_USE_MXFP8_LMHEAD"):
@@ -170,7 +171,7 @@ class QuantizedLogitsProcessor(LogitsProcessor):
                 print(f"{_TAG} VLLM_USE_MXFP8_LMHEAD: the gfx950 kernel needs K % 128 == 0 "
                       f"(got K={Kdim}), falling back to int8", file=_sys.stderr, flush=True)
             else:
-                self._init_mxfp8(lm_head, w, _sys)
+                self._init_cached("mxfp8", lm_head, w, _sys, lambda: self._init_mxfp8(lm_head, w, _sys))
                 return
 
         if _env_bool("VLLM_USE_FP8_LMHEAD"):
@@ -178,7 +179,7 @@ class QuantizedLogitsProcessor(LogitsProcessor):
                 print(f"{_TAG} VLLM_USE_FP8_LMHEAD requires gfx950 (MI355X), falling back to int8",
                       file=_sys.stderr, flush=True)
             else:
-                self._init_fp8(lm_head, w, _sys)
+                self._init_cached("fp8", lm_head, w, _sys, lambda: self._init_fp8(lm_head, w, _sys))
                 return
 
         if _env_bool("VLLM_USE_W8A8_LMHEAD"):
@@ -186,7 +187,7 @@ class QuantizedLogitsProcessor(LogitsProcessor):
                 print(f"{_TAG} VLLM_USE_W8A8_LMHEAD requires gfx950 (MI355X), falling back to w8a16 int8",
                       file=_sys.stderr, flush=True)
             else:
-                self._init_w8a8(lm_head, w, _sys)
+                self._init_cached("w8a8", lm_head, w, _sys, lambda: self._init_w8a8(lm_head, w, _sys))
                 return
 
         if not ok or not _kernel_k_ok("int8", Kdim):
@@ -195,7 +196,46 @@ class QuantizedLogitsProcessor(LogitsProcessor):
             print(f"{_TAG} lm_head left unquantized: the int8 kernel needs a gfx950 (MI355X) "
                   f"device and K % 128 == 0 (got K={Kdim})", file=_sys.stderr, flush=True)
             return
-        self._init_int8_weights(lm_head, w, _sys, ok)
+        self._init_cached("int8", lm_head, w, _sys, lambda: self._init_int8_weights(lm_head, w, _sys, ok))
+
+    def _init_cached(self, mode, lm_head, w, _sys, quantize) -> None:
+        """Quantize, or, with VQK_LMHEAD_CACHE_DIR set (an extension; the reference always
+        quantizes at load), load the packed weight from that directory when a file made
+        from this very weight exists, and write one after quantizing otherwise."""
+        d = os.environ.get("VQK_LMHEAD_CACHE_DIR", "")
+        path = _ckpt.cache_path(d, mode, int(w.shape[0]), int(w.shape[1])) if d else ""
+        if d:
+            try:
+                if _ckpt.load_quantized(lm_head, path, mode=mode, source=w) == mode:
+                    self._install_handles(mode, lm_head)
+                    print(f"{_TAG} lm_head {mode} weights loaded from {path}", file=_sys.stderr, flush=True)
+                    return
+            except Exception as e:  # an unreadable cache file: quantize as usual
+                print(f"{_TAG} lm_head cache {path} not used ({e})", file=_sys.stderr, flush=True)
+        quantize()
+        if d:
+            try:
+                _ckpt.save_quantized(lm_head, path, source=w)
+                print(f"{_TAG} lm_head {mode} weights written to {path}", file=_sys.stderr, flush=True)
+            except Exception as e:
+                print(f"{_TAG} lm_head cache {path} not written ({e})", file=_sys.stderr, flush=True)
+
+    @staticmethod
+    def _install_handles(mode, lm_head) -> None:
+        """The non-tensor attributes each mode's init leaves on lm_head."""
+        if mode == "int8":
+            lm_head._int8_use_thor = True
+            lm_head._int8_block_m = 128
+            lm_head._int8_block_k = 256
+            lm_head._int8_gemm_kernel, lm_head._int8_n_bucket = K_._make_thor_gemm_kernel()
+        elif mode == "w8a8":
+            lm_head._w8a8_gemm_kernel, lm_head._w8a8_n_bucket = K_._make_thor_w8a8_gemm_kernel()
+        elif mode == "fp8":
+            lm_head._fp8_gemm_kernel, lm_head._fp8_n_bucket = K_._make_thor_fp8_gemm_kernel()
+        elif mode == "mxfp8":
+            lm_head._mxfp8_gemm_kernel, lm_head._mxfp8_n_bucket = K_._make_thor_mxfp8_gemm_kernel()
+        elif mode == "mxfp4":
+            lm_head._mxfp4_gemm_kernel, lm_head._mxfp4_n_bucket = K_._make_thor_mxfp4_gemm_kernel()
 
     def _init_int8_weights(self, lm_head, w, _sys, is_thor: bool) -> None:
         """Per-row INT8 weight-only (reference _quant.py:245-276)."""
