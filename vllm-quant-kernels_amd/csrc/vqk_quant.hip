@@ -112,21 +112,25 @@ __global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt
   }
 }
 
-// Per-tensor INT8 activation quantization: a single workgroup (the activation is tiny),
-// two passes (amax, then codes), 8 consecutive elements per thread and step when rows
-// allow 16-byte loads.  Codes are rint(x / s) exactly (rint_div_i8), clamped to +-127.
+// Per-tensor INT8 activation quantization.  The activation is small (B x K of a decode
+// step), so every workgroup computes the whole tensor's amax itself (the re-reads come from
+// L2) and then quantizes its own share: one launch, no cross-workgroup exchange, and as
+// many CUs as shares.  8 consecutive elements per thread and step when rows allow 16-byte
+// loads.  Codes are rint(x / s) exactly (rint_div_i8), clamped to +-127.
 template <int DT>
-__global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int64_t ldx, int64_t B,
-                                                               int64_t K, int vec, int8_t* xq, float* xs) {
+__global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int64_t ldx, int64_t B, int64_t K,
+                                                              int vec, int8_t* xq, float* xs) {
   __shared__ float red[16];
-  const int64_t per_row = K / 8, total = B * per_row;
+  // 32-bit indices (B * K / 8 < 2^31 on the vector path): a 64-bit division per step
+  // would cost more than the loads
+  const int per_row = (int)(K / 8), total = (int)B * per_row;
   float m = 0.f;
   if (vec) {
 #pragma unroll 4
-    for (int64_t c = threadIdx.x; c < total; c += blockDim.x) {
-      const int64_t b = c / per_row, k8 = c - b * per_row;
+    for (int c = threadIdx.x; c < total; c += blockDim.x) {
+      const int b = c / per_row, k8 = c - b * per_row;
       float v[8];
-      load_run<DT, 8>(x, b * ldx + 8 * k8, true, v);
+      load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
     }
@@ -138,27 +142,30 @@ __global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int
   const float s = fmaxf(m / 127.0f, 1e-12f);
   const float r = 1.0f / s;
   if (vec) {
-#pragma unroll 4
-    for (int64_t c = threadIdx.x; c < total; c += blockDim.x) {
-      const int64_t b = c / per_row, k8 = c - b * per_row;
+    // this workgroup's share of the 8-element chunks
+    const int share = (total + gridDim.x - 1) / gridDim.x;
+    const int c0 = blockIdx.x * share, c1 = min(total, c0 + share);
+#pragma unroll 2
+    for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
+      const int b = c / per_row, k8 = c - b * per_row;
       float v[8];
-      load_run<DT, 8>(x, b * ldx + 8 * k8, true, v);
+      load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v);
       uint32_t w[2] = {0u, 0u};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float q = fminf(fmaxf(rint_div_i8(v[e], s, r), -127.f), 127.f);
         w[e >> 2] |= ((uint32_t)(int)q & 0xFFu) << (8 * (e & 3));
       }
-      *(uint2*)(xq + b * K + 8 * k8) = make_uint2(w[0], w[1]);
+      *(uint2*)(xq + (int64_t)b * K + 8 * k8) = make_uint2(w[0], w[1]);
     }
-  } else {
+  } else if (blockIdx.x == 0) {
     for (int64_t b = 0; b < B; ++b)
       for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
         const float q = fminf(fmaxf(rint_div_i8(load_dt<DT>(x, b * ldx + k), s, r), -127.f), 127.f);
         xq[b * K + k] = (int8_t)(int)q;
       }
   }
-  if (threadIdx.x == 0) *xs = s;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *xs = s;
 }
 
 __global__ void act_cast_e4m3_kernel(const void* x, int dt, int64_t ldx, int64_t B, int64_t K, uint8_t* xq) {
@@ -242,13 +249,21 @@ extern "C" int vqk_act_quant_int8(const void* x, int x_dtype, int64_t ldx, int64
   if (!x || !xq || !xs || !dt_ok(x_dtype) || B < 0 || K < 1 || ldx < K) return VQK_EINVAL;
   if (B == 0) return VQK_OK;
   const int es = (x_dtype == VQK_F32) ? 4 : 2;
-  const int vec = (K % 8 == 0 && ((uintptr_t)x & 15) == 0 && (ldx * es) % 16 == 0 && ((uintptr_t)xq & 7) == 0) ? 1 : 0;
+  const int vec = (K % 8 == 0 && ((uintptr_t)x & 15) == 0 && (ldx * es) % 16 == 0 && ((uintptr_t)xq & 7) == 0 &&
+                   B * (K / 8) < (int64_t)INT32_MAX) ? 1 : 0;
+  // one share per ~8192 elements, at most 32 (each workgroup re-reads the whole tensor for
+  // the amax, so large activations take fewer shares)
+  const int64_t n = B * K;
+  int grid = (int)((n + 8191) / 8192);
+  if (grid > 32) grid = 32;
+  if (n > ((int64_t)1 << 22)) grid = 4;
+  if (!vec || grid < 1) grid = 1;
   if (x_dtype == VQK_F32)
-    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F32>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F32>, dim3(grid), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
   else if (x_dtype == VQK_F16)
-    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F16>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_F16>, dim3(grid), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
   else
-    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_BF16>, dim3(1), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
+    hipLaunchKernelGGL(act_quant_int8_kernel<VQK_BF16>, dim3(grid), dim3(1024), 0, (hipStream_t)stream, x, ldx, B, K, vec, xq, xs);
   return finish();
 }
 
