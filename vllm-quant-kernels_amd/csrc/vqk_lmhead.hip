@@ -57,6 +57,9 @@
 #ifndef VQK_LM_BALANCE
 #define VQK_LM_BALANCE 8   // batch groups up to this size: shrink the grid so every wave
 #endif                     // streams the same number of tiles
+#ifndef VQK_LM_PAIR
+#define VQK_LM_PAIR 1  // two batch groups: one launch of XCD-paired workgroups (1) or two launches (0)
+#endif
 #ifndef VQK_LM_SC_POLICY
 // cache policy of the MX scale pieces: temporal.  A stage reads 8-16 bytes of each row's
 // scale line and the following stages read the rest of that line, so the line must stay in
@@ -137,6 +140,11 @@ struct LmArgs {
   int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
   int xs_off;           // MX: LDS byte offset of the activation scales
   int xvec;             // 1 when activation rows (x or xq) allow 16-byte loads
+  // two batch groups in one launch (paired workgroups, see lmhead_lds_kernel): 2, else 1;
+  // the second group's offsets from the first's pointers, and its row count
+  int ngrp;
+  int64_t g1_x, g1_xq, g1_xsq, g1_out, g1_acc;
+  int g1_Bg;
   // fused Gumbel-argmax epilogue (the sampling form only)
   const float* stemp;   // [Bg] temperatures or null (greedy)
   const void* sseeds;   // [Bg] int32 or int64 seeds
@@ -825,11 +833,31 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
 }
 
 template <int MODE, int NCT, int S, bool SMP = false>
-__global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
+__global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float red[17];
+  // Two batch groups in one launch: workgroups b and b + 8 (the same XCD under the
+  // round-robin dispatch of workgroups to the 8 XCDs) stream the same weight tiles in the
+  // same order for different batch rows, so the second reader of each line finds it in
+  // that XCD's L2 or in the last-level cache: the weight crosses HBM about once instead of
+  // once per group.
+  LmArgs a = a0;
+  int bid = blockIdx.x, nwg = gridDim.x;
+  if (a0.ngrp == 2) {
+    const int grp = (bid >> 3) & 1;
+    bid = ((bid >> 4) << 3) | (bid & 7);
+    nwg = gridDim.x >> 1;
+    if (grp) {
+      a.x = a0.x ? (const void*)((const char*)a0.x + a0.g1_x) : nullptr;
+      a.xq = a0.xq ? a0.xq + a0.g1_xq : nullptr;
+      a.xsq = a0.xsq ? a0.xsq + a0.g1_xsq : nullptr;
+      a.out = a0.out + a0.g1_out;
+      a.acc = a0.acc ? a0.acc + a0.g1_acc : nullptr;
+      a.Bg = a0.g1_Bg;
+    }
+  }
   const int K = a.K;
   const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;
   uint8_t* lds = smem;
@@ -843,8 +871,8 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a) {
   const int r = lane & 15, g = lane >> 4;
   const XPtr<MODE, NCT> xp = x_pointers<MODE, NCT>(a, lds, lds_xs, g, r);
   const int ntiles = (a.M + 15) >> 4;
-  const int wid = blockIdx.x * 4 + wave;
-  const int total = gridDim.x * 4;
+  const int wid = bid * 4 + wave;
+  const int total = nwg * 4;
   if (wid >= ntiles) {
     if (SMP && (threadIdx.x & 63) < (unsigned)a.Bg) a.skeys[(int64_t)(threadIdx.x & 63) * total + wid] = 0ull;
     return;
@@ -1133,6 +1161,9 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.out_vec = (((uintptr_t)out & 7) == 0 && (ldo & 3) == 0) ? 1 : 0;
     a.xs_val = xs_val;
     a.xs_dev = xs_dev;
+    a.ngrp = 1;
+    a.g1_x = a.g1_xq = a.g1_xsq = a.g1_out = a.g1_acc = 0;
+    a.g1_Bg = Bg;
     a.stemp = smp ? smp->temp : nullptr;
     a.sseeds = smp ? smp->seeds : nullptr;
     a.sseed64 = smp ? smp->seed64 : 0;
@@ -1168,6 +1199,32 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       }
       const int nct_l = (Bg + 15) / 16;
       int rcl;
+      if (ngroups == 2 && b0 == 0 && !smp && VQK_LM_PAIR) {
+        // both groups in one launch: half the CUs each, in XCD-aligned runs of 8
+        // workgroups; every wave of the launch gets the same number of tiles (+-1)
+        int gpg = (ncu / 2) & ~7;
+        const int maxg = (((ntiles + 3) / 4) + 7) & ~7;
+        if (gpg > maxg) gpg = maxg;
+        if (gpg >= 8) {
+          const int xes2 = (xdt == VQK_F32) ? 4 : 2;
+          a.ngrp = 2;
+          a.g1_x = (int64_t)gsize * ldx * xes2;
+          a.g1_xq = (int64_t)gsize * K;
+          a.g1_xsq = (int64_t)gsize * (K / 32);
+          a.g1_out = (int64_t)gsize * ldo;
+          a.g1_acc = (int64_t)gsize * M;
+          a.g1_Bg = (int)(B - gsize);
+          const int nct_p = (gsize + 15) / 16;  // the larger group's column tiles
+          if constexpr (MODE == M_W8A16) {
+            rcl = launch_lds<MODE, 1>(a, stages, lds_l, 2 * gpg, st);
+          } else {
+            rcl = (nct_p == 1) ? launch_lds<MODE, 1>(a, stages, lds_l, 2 * gpg, st)
+                               : launch_lds<MODE, 2>(a, stages, lds_l, 2 * gpg, st);
+          }
+          if (rcl) return rcl;
+          break;
+        }
+      }
       if (smp) {
         if (4 * (int64_t)grid_l > smp->slots_per_row) return VQK_EWORKSPACE;
         if constexpr (MODE == M_W8A16) {
