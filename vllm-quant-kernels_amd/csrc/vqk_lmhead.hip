@@ -66,6 +66,9 @@
 // L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
 #define VQK_LM_SC_POLICY 0
 #endif
+#ifndef VQK_LM_EARLY
+#define VQK_LM_EARLY 0     // bit MODE set: issue a wave's first ring stages before the activation prologue
+#endif
 #ifndef VQK_LM_NT_LDS
 #define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
 #endif
@@ -188,8 +191,15 @@ __device__ __forceinline__ void smp_lane_init(const LmArgs& a, int lane, SmpLane
 // MX scales: dword xs_off/4 + b*xsr + (mi/4)*4 + g holds byte (mi % 4) for fragment mi.
 // Lanes of columns b >= Bg read row Bg-1 (their results are never stored), so no zero
 // fragments are needed.
+// A compile-time bool carried by value into a generic lambda (hoists a uniform branch out
+// of an unrolled loop).
+template <bool B_>
+struct BoolTag {
+  static constexpr bool value = B_;
+};
+
 template <int MODE, int DT>
-__device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
+__device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, float* lds_red) {
   typedef ModeTraits<MODE> T;
   const int tid = threadIdx.x, nth = blockDim.x;
   const int K = a.K, Bg = a.Bg;
@@ -234,52 +244,136 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
   const float xs_inv = 1.0f / xs_w8a8;  // W8A8: reciprocal for rint_div_i8 (IEEE division)
 
   if constexpr (T::MX) {
-    // one 32-element MX group per work item; its 32 bytes land in two 16-byte halves of the
-    // fragments of lanes g = 2(j%2) and 2(j%2)+1 (j = group % 4), at byte 16*(j/2)
     const int G = K / 32;
-    for (int f = tid; f < G * Bg; f += nth) {
-      const int b = f % Bg, grp = f / Bg;
-      const int mi = grp >> 2, j = grp & 3;
-      uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-      uint32_t sbyte;
-      if (a.xq) {
+    if (a.xq) {
+      // pre-quantized bytes: one 32-element group (and its scale byte) per work item
+      for (int f = tid; f < G * Bg; f += nth) {
+        const int b = f % Bg, grp = f / Bg;
+        const int mi = grp >> 2, j = grp & 3;
         const uint8_t* src = a.xq + (int64_t)b * K + 32 * grp;
+        uint4 t0, t1;
         if (a.xvec) {
-          const uint4 t0 = ((const uint4*)src)[0], t1 = ((const uint4*)src)[1];
-          v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
-          v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+          t0 = ((const uint4*)src)[0];
+          t1 = ((const uint4*)src)[1];
         } else {
+          uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
 #pragma unroll
           for (int e = 0; e < 32; ++e) v[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+          t0 = make_uint4(v[0], v[1], v[2], v[3]);
+          t1 = make_uint4(v[4], v[5], v[6], v[7]);
         }
-        sbyte = a.xsq[(int64_t)b * G + grp];
-      } else {
-        const int64_t xo = (int64_t)b * a.ldx + 32 * grp;
-        float xv[32];
-        load_run<DT, 32>(a.x, xo, a.xvec != 0, xv);
-        float amax = 0.f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(xv[e]));
-        int kx = mx_exponent(amax, 448.0f);
-        float sc = exp2i(kx);
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-          float y = fminf(fmaxf(xv[e] / sc, -448.0f), 448.0f);
-          v[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
-        }
-        sbyte = (uint32_t)(kx + 127);
+        // the group's 32 bytes land in two 16-byte halves of the fragments of lanes
+        // g = 2(j%2) and 2(j%2)+1 (j = group % 4), at byte 16*(j/2)
+        uint8_t* d0 = lds + (size_t)b * a.xr + (size_t)(mi * 4 + 2 * (j & 1)) * T::FB + 16 * (j >> 1);
+        *(uint4*)d0 = t0;
+        *(uint4*)(d0 + T::FB) = t1;
+        uint8_t* sdst = (uint8_t*)(lds_xs + (size_t)b * a.xsr + (mi >> 2) * 4 + j) + (mi & 3);
+        *sdst = a.xsq[(int64_t)b * G + grp];
       }
-      const int g0 = 2 * (j & 1), off = 16 * (j >> 1);
-      uint8_t* d0 = lds + (size_t)b * a.xr + (size_t)(mi * 4 + g0) * T::FB + off;
-      uint8_t* d1 = d0 + T::FB;
-      *(uint4*)d0 = make_uint4(v[0], v[1], v[2], v[3]);
-      *(uint4*)d1 = make_uint4(v[4], v[5], v[6], v[7]);
-      uint8_t* sdst = (uint8_t*)(lds_xs + (size_t)b * a.xsr + (mi >> 2) * 4 + j) + (mi & 3);
-      *sdst = (uint8_t)sbyte;
+    } else {
+      // Quantize from the float activations: four lanes per group, 8 elements each (the
+      // group's amax takes two lane exchanges), U items per thread and round with every
+      // load of the round issued before the first encoding.  Lane quarter l of a group
+      // writes bytes 8(l%2).. of half l/2 of the layout above.
+      auto quantize = [&](auto vtag) {
+        constexpr bool V = decltype(vtag)::value;
+        constexpr int U = 4;
+        const int nit = 4 * G * Bg;  // a multiple of 4: a group's lanes share every trip
+        for (int i0 = tid; i0 < nit; i0 += U * nth) {
+          int f[U], l[U];
+          bool ok[U];
+          float xv[U][8];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int it = i0 + u * nth;
+            ok[u] = it < nit;  // the same for the 4 lanes of a group
+            const int ic = ok[u] ? it : (it & 3);
+            f[u] = ic >> 2;
+            l[u] = ic & 3;
+            const int b = f[u] % Bg, grp = f[u] / Bg;
+            load_run<DT, 8>(a.x, (int64_t)b * a.ldx + 32 * grp + 8 * l[u], V, xv[u]);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            float amax = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xv[u][e]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1));
+            amax = fmaxf(amax, __shfl_xor(amax, 2));
+            const int kx = mx_exponent(amax, 448.0f);
+            // x / 2^kx as x * 2^-kx: the same correctly rounded value (2^-kx is exact)
+            const float isc = exp2i(-kx);
+            uint32_t v[2] = {0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float y = fminf(fmaxf(xv[u][e] * isc, -448.0f), 448.0f);
+              v[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
+            }
+            if (!ok[u]) continue;
+            const int b = f[u] % Bg, grp = f[u] / Bg;
+            const int mi = grp >> 2, j = grp & 3;
+            const int gl = 2 * (j & 1) + (l[u] >> 1), off = 16 * (j >> 1) + 8 * (l[u] & 1);
+            *(uint2*)(lds + (size_t)b * a.xr + (size_t)(mi * 4 + gl) * T::FB + off) = make_uint2(v[0], v[1]);
+            if (l[u] == 0) {
+              uint8_t* sdst = (uint8_t*)(lds_xs + (size_t)b * a.xsr + (mi >> 2) * 4 + j) + (mi & 3);
+              *sdst = (uint8_t)(kx + 127);
+            }
+          }
+        }
+      };
+      if (a.xvec) quantize(BoolTag<true>{});
+      else quantize(BoolTag<false>{});
     }
+  } else if (MODE != M_W8A16 && !a.xq) {
+    // W8A8 (16-element fragments) or FP8 (32): quantize from the exact float, in items of 8
+    // consecutive elements (a fragment's runs of 16 split in two), QU items per thread and
+    // round with every load issued before the first conversion.
+    auto quantize = [&](auto vtag) {
+      constexpr bool V = decltype(vtag)::value;
+      constexpr int QU = 4, IPF = T::FB / 8;
+      const int nit = nfrag * IPF;
+      for (int i0 = tid; i0 < nit; i0 += QU * nth) {
+        float xv[QU][8];
+        int fb[QU], fgm[QU], sub[QU];
+        bool ok[QU];
+#pragma unroll
+        for (int u = 0; u < QU; ++u) {
+          const int it = i0 + u * nth;
+          ok[u] = it < nit;
+          const int ic = ok[u] ? it : nit - 1;
+          const int f = ic / IPF;
+          sub[u] = ic - f * IPF;
+          fb[u] = f % Bg;
+          fgm[u] = f / Bg;
+          const int g = fgm[u] & 3, mi = fgm[u] >> 2;
+          load_run<DT, 8>(a.x, (int64_t)fb[u] * a.ldx + frag_k<MODE>(mi, g, 16 * (sub[u] >> 1)) + 8 * (sub[u] & 1),
+                          V, xv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < QU; ++u) {
+          uint32_t v[2] = {0u, 0u};
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            uint32_t byte;
+            if (MODE == M_W8A8) {
+              float q = rint_div_i8(xv[u][p], xs_w8a8, xs_inv);
+              q = fminf(fmaxf(q, -127.f), 127.f);
+              byte = (uint32_t)(uint8_t)(int8_t)(int)q;
+            } else {
+              byte = f32_to_e4m3(xv[u][p]);
+            }
+            v[p >> 2] |= byte << (8 * (p & 3));
+          }
+          if (ok[u]) *(uint2*)(lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB + 8 * sub[u]) = make_uint2(v[0], v[1]);
+        }
+      }
+    };
+    if (a.xvec) quantize(BoolTag<true>{});
+    else quantize(BoolTag<false>{});
   } else {
-    // U fragments per thread per round: every load of the round is issued before the
-    // first conversion, so a round costs one memory latency.
+    // W8A16 (fp16 copied as raw bits) or pre-quantized bytes: U fragments per thread per
+    // round, every load of the round issued before the first store, so a round costs one
+    // memory latency.
     constexpr int U = (MODE == M_FP8) ? 1 : 4;
     const bool vec = a.xvec != 0;
     for (int f0 = tid; f0 < nfrag; f0 += U * nth) {
@@ -312,7 +406,7 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
 #pragma unroll
         for (int u = 0; u < U; ++u)
           if (ok[u]) *(uint4*)(lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB) = raw[u];
-      } else if (a.xq) {
+      } else {
         // pre-quantized bytes: element p of the fragment is row element frag_k(p), which
         // comes in runs of 16 consecutive bytes
         uint4 raw[U][T::FB / 16];
@@ -338,40 +432,6 @@ __device__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32_t* lds_xs, floa
           uint8_t* dst = lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB;
 #pragma unroll
           for (int r = 0; r < T::FB / 16; ++r) *(uint4*)(dst + 16 * r) = raw[u][r];
-        }
-      } else {
-        // W8A8 (16 elements) or FP8 (32 = two runs of 16): quantize from the exact float
-        float xv[U][T::FB];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int g = fgm[u] & 3, mi = fgm[u] >> 2;
-#pragma unroll
-          for (int r = 0; r < T::FB / 16; ++r) {
-            float run[16];
-            load_run<DT, 16>(a.x, (int64_t)fb[u] * a.ldx + frag_k<MODE>(mi, g, 16 * r), vec, run);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) xv[u][16 * r + e] = run[e];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          uint32_t v[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-#pragma unroll
-          for (int p = 0; p < T::FB; ++p) {
-            uint32_t byte;
-            if (MODE == M_W8A8) {
-              float q = rint_div_i8(xv[u][p], xs_w8a8, xs_inv);
-              q = fminf(fmaxf(q, -127.f), 127.f);
-              byte = (uint32_t)(uint8_t)(int8_t)(int)q;
-            } else {
-              byte = f32_to_e4m3(xv[u][p]);
-            }
-            v[p >> 2] |= byte << (8 * (p & 3));
-          }
-          if (!ok[u]) continue;
-          uint8_t* dst = lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB;
-          *(uint4*)dst = make_uint4(v[0], v[1], v[2], v[3]);
-          if (T::FB == 32) *(uint4*)(dst + 16) = make_uint4(v[4], v[5], v[6], v[7]);
         }
       }
     }
@@ -873,36 +933,23 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
   uint8_t* lds = smem;
   uint32_t* lds_xs = (uint32_t*)(smem + a.xs_off);
 
-  stage_x<MODE>(a, lds, lds_xs, red);
-  const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
-
+  constexpr bool EARLY = ((VQK_LM_EARLY >> MODE) & 1) != 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int r = lane & 15, g = lane >> 4;
-  const XPtr<MODE, NCT> xp = x_pointers<MODE, NCT>(a, lds, lds_xs, g, r);
   const int ntiles = (a.M + 15) >> 4;
   const int wid = bid * 4 + wave;
   const int total = nwg * 4;
-  if (wid >= ntiles) {
-    if (SMP && (threadIdx.x & 63) < (unsigned)a.Bg) a.skeys[(int64_t)(threadIdx.x & 63) * total + wid] = 0ull;
-    return;
-  }
-  const int my_tiles = (ntiles - 1 - wid) / total + 1;
+  const bool live = wid < ntiles;
+  const int my_tiles = live ? (ntiles - 1 - wid) / total + 1 : 0;
   const int SPT = KB >> 8;  // stages per tile (KB % 256 == 0, host guarantees)
   const int nst = my_tiles * SPT;
   uint8_t* ring = smem + a.lds_x_bytes + wave * (S * G::SLOT);
 
-  // lane (r, g) reads row r: its 4 pieces of a stage, rotated by 16r within the row's 256 B
-  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
-  const uint8_t* wpc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) wpc[i] = ring + rbase + ((64 * i + 16 * g + 16 * r) & 255);
-  const uint8_t* spc = ring + LDS_STAGE + G::SB * r;  // MX: row r's scale bytes of a stage
-
   // issue side: stage iq of the wave = (itile, iks)
   IssueOffsets<MODE> io;
   int itile = wid, iks = 0, iq = 0;
-  issue_offsets<MODE>(a, KB, itile, lane, io);
+  issue_offsets<MODE>(a, KB, itile, lane, io);  // (idle waves, nst = 0, never use them)
   auto advance_issue = [&]() {
     ++iq;
     if (++iks == SPT) {
@@ -911,13 +958,36 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
       if (iq < nst) issue_offsets<MODE>(a, KB, itile, lane, io);
     }
   };
+  auto fill_ring = [&]() {
 #pragma unroll
-  for (int s0 = 0; s0 < S; ++s0) {
-    if (iq < nst) {
-      issue_stage<MODE>(a, KB, itile, iks, ring + s0 * G::SLOT, lane, io);
-      advance_issue();
+    for (int s0 = 0; s0 < S; ++s0) {
+      if (iq < nst) {
+        issue_stage<MODE>(a, KB, itile, iks, ring + s0 * G::SLOT, lane, io);
+        advance_issue();
+      }
     }
+  };
+  // The ring lies past the activations in LDS: its first stages may stream in while the
+  // prologue stages the activations.
+  if (EARLY) fill_ring();
+
+  stage_x<MODE>(a, lds, lds_xs, red);
+  const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
+
+  if (!live) {
+    if (SMP && (threadIdx.x & 63) < (unsigned)a.Bg) a.skeys[(int64_t)(threadIdx.x & 63) * total + wid] = 0ull;
+    return;
   }
+  const XPtr<MODE, NCT> xp = x_pointers<MODE, NCT>(a, lds, lds_xs, g, r);
+
+  // lane (r, g) reads row r: its 4 pieces of a stage, rotated by 16r within the row's 256 B
+  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
+  const uint8_t* wpc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wpc[i] = ring + rbase + ((64 * i + 16 * g + 16 * r) & 255);
+  const uint8_t* spc = ring + LDS_STAGE + G::SB * r;  // MX: row r's scale bytes of a stage
+
+  if (!EARLY) fill_ring();
 
   Acc<MODE, NCT> acc;
 #pragma unroll

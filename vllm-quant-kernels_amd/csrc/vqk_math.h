@@ -107,23 +107,18 @@ __device__ __forceinline__ float rint_div_i8(float x, float s, float r) {
 //   trick and re-bias the exponent from 127 to 7.  Codes above 0x7E mean "rounded past
 //   448", which is NaN in this format.
 __device__ __forceinline__ uint8_t f32_to_e4m3(float x) {
-  uint32_t b = bits_f32(x);
-  uint32_t sign = (b >> 24) & 0x80u;
-  uint32_t a = b & 0x7FFFFFFFu;
-  uint32_t code;
-  if (a > 0x7F800000u) {
-    code = 0x7Fu;  // NaN
-  } else if (a < 0x3C800000u) {  // |x| < 2^-6
-    float s = __uint_as_float(a) * 512.0f;
-    code = (uint32_t)__builtin_rintf(s);
-  } else if (a >= 0x43E80000u) {  // |x| > 464 (0x43E80000 = 464.0) or exactly 464
-    code = (a == 0x43E80000u) ? 0x7Eu : 0x7Fu;
-  } else {
-    uint32_t odd = (a >> 20) & 1u;
-    uint32_t r = a + 0x7FFFFu + odd;
-    code = (r >> 20) - ((127u - 7u) << 3);
-    if (code > 0x7Eu) code = 0x7Fu;
-  }
+  // Both cases are computed and one is selected (no branches: this runs per element in
+  // unrolled loops).  The normal-range code saturates at 0x7F, which covers NaN, +-inf and
+  // everything that rounds past 448 (|x| > 464 or NaN give codes >= 0x7F).
+  const uint32_t b = bits_f32(x);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t a = b & 0x7FFFFFFFu;
+  const uint32_t odd = (a >> 20) & 1u;
+  const uint32_t cn = min(((a + 0x7FFFFu + odd) >> 20) - ((127u - 7u) << 3), 0x7Fu);
+  // |x| < 2^-6: rint(|x| * 2^9) in [0, 8] (the operand is clamped so the conversion
+  // stays in range whichever case is selected)
+  const uint32_t cs = (uint32_t)__builtin_rintf(fminf(__uint_as_float(a), 0.015625f) * 512.0f);
+  const uint32_t code = (a < 0x3C800000u) ? cs : cn;
   return (uint8_t)(code | sign);
 }
 

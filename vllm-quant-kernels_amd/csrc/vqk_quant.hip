@@ -91,14 +91,14 @@ __global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt
   amax = fmaxf(amax, __shfl_xor(amax, 1));
   amax = fmaxf(amax, __shfl_xor(amax, 2));
   const int k = mx_exponent(amax, fp4 ? 6.0f : 448.0f);
-  const float sc = exp2i(k);
+  const float isc = exp2i(-k);  // x / 2^k as x * 2^-k: the same correctly rounded value
   if (!live) return;
   if (part == 0) scales[row * G + grp] = (uint8_t)(k + 127);
   if (!fp4) {
     uint32_t w[2] = {0, 0};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float y = fminf(fmaxf(v[e] / sc, -448.f), 448.f);
+      const float y = fminf(fmaxf(v[e] * isc, -448.f), 448.f);
       w[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
     }
     uint32_t* dst = (uint32_t*)(q + row * K + grp * 32 + part * 8);
@@ -107,7 +107,7 @@ __global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt
   } else {
     uint32_t w = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w |= f32_to_e2m1(v[e] / sc) << (4 * e);
+    for (int e = 0; e < 8; ++e) w |= f32_to_e2m1(v[e] * isc) << (4 * e);
     *(uint32_t*)(q + row * (K / 2) + grp * 16 + part * 4) = w;
   }
 }
