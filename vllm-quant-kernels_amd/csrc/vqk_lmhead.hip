@@ -66,8 +66,22 @@
 // L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
 #define VQK_LM_SC_POLICY 0
 #endif
-#ifndef VQK_LM_EARLY
-#define VQK_LM_EARLY 0     // bit MODE set: issue a wave's first ring stages before the activation prologue
+#ifndef VQK_LM_WPE
+// >0: amdgpu_waves_per_eu(1, VQK_LM_WPE) on the LDS-staged kernel.  Its LDS footprint
+// allows one workgroup (one wave per SIMD) per CU, so the compiler may spend registers
+// on keeping LDS reads in flight instead of aiming for an occupancy that cannot occur
+// (measured: without it the W8A16 loop waits on every fragment read once the held logits
+// take their registers, 113 -> 131 us at batch 1).
+#define VQK_LM_WPE 2
+#endif
+#if VQK_LM_WPE > 0
+#define VQK_LM_WPE_ATTR __attribute__((amdgpu_waves_per_eu(1, VQK_LM_WPE)))
+#else
+#define VQK_LM_WPE_ATTR
+#endif
+#ifndef VQK_LM_DEFER
+#define VQK_LM_DEFER 16    // logits held in registers for up to this many tiles per wave
+                           // (measured: 32 slows batch 1 by ~1 us); 0: stored tile by tile
 #endif
 #ifndef VQK_LM_NT_LDS
 #define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
@@ -642,10 +656,10 @@ __device__ __forceinline__ void row_scales(const LmArgs& a, int m0, int lane, fl
 
 template <int MODE, int NCT>
 __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, int m0, int lane,
-                                         float xs_w8a8, const float (&sc)[4], SmpLane<NCT>* sl = nullptr) {
+                                         float xs_w8a8, const float (&sc)[4], uint2 (&ov)[NCT],
+                                         SmpLane<NCT>* sl = nullptr) {
   const int g = lane >> 4, j = lane & 15;
   const int mr = m0 + 4 * g;
-  const bool full = (mr + 3 < a.M);
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
     const int b = ct * 16 + j;
@@ -682,14 +696,7 @@ __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, i
           }
         }
       }
-      uint16_t* op = a.out + (int64_t)b * a.ldo + mr;
-      if (full && a.out_vec) {
-        *(uint2*)op = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (mr + e < a.M) op[e] = o[e];
-      }
+      ov[ct] = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
       if (MODE == M_W8A8) {
         if (a.acc) {
           int32_t* ap = a.acc + (int64_t)b * a.M + mr;
@@ -700,6 +707,28 @@ __device__ __forceinline__ void epilogue(Acc<MODE, NCT>& acc, const LmArgs& a, i
       }
     }
     acc.zero(ct);
+  }
+}
+
+// Store one tile's packed logits (lane (j, g): batch row ct*16 + j, rows mr..mr+3 of the
+// tile at m0, mr = m0 + 4g), clipping the ragged last tile.
+template <int NCT>
+__device__ __forceinline__ void store_tile(const LmArgs& a, int m0, int lane, const uint2 (&ov)[NCT]) {
+  const int g = lane >> 4, j = lane & 15;
+  const int mr = m0 + 4 * g;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int b = ct * 16 + j;
+    if (b >= a.Bg) continue;
+    uint16_t* op = a.out + (int64_t)b * a.ldo + mr;
+    if (mr + 3 < a.M && a.out_vec) {
+      *(uint2*)op = ov[ct];
+    } else {
+      const uint32_t w[2] = {ov[ct].x, ov[ct].y};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (mr + e < a.M) op[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    }
   }
 }
 
@@ -773,7 +802,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) l
     if (c0 + D == CPR) {
       float sc[4];
       row_scales<MODE>(a, (wid + tq * total) * 16, lane, sc);
-      epilogue<MODE, NCT>(acc, a, (wid + tq * total) * 16, lane, xs_w8a8, sc);
+      uint2 ov[NCT];
+      epilogue<MODE, NCT>(acc, a, (wid + tq * total) * 16, lane, xs_w8a8, sc, ov);
+      store_tile<NCT>(a, (wid + tq * total) * 16, lane, ov);
     }
   }
 }
@@ -903,7 +934,7 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
 }
 
 template <int MODE, int NCT, int S, bool SMP = false>
-__global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
+__global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs a0) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -933,7 +964,6 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
   uint8_t* lds = smem;
   uint32_t* lds_xs = (uint32_t*)(smem + a.xs_off);
 
-  constexpr bool EARLY = ((VQK_LM_EARLY >> MODE) & 1) != 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int r = lane & 15, g = lane >> 4;
@@ -967,9 +997,6 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
       }
     }
   };
-  // The ring lies past the activations in LDS: its first stages may stream in while the
-  // prologue stages the activations.
-  if (EARLY) fill_ring();
 
   stage_x<MODE>(a, lds, lds_xs, red);
   const float xs_w8a8 = (MODE == M_W8A8) ? red[16] : 0.f;
@@ -987,13 +1014,20 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
   for (int i = 0; i < 4; ++i) wpc[i] = ring + rbase + ((64 * i + 16 * g + 16 * r) & 255);
   const uint8_t* spc = ring + LDS_STAGE + G::SB * r;  // MX: row r's scale bytes of a stage
 
-  if (!EARLY) fill_ring();
+  fill_ring();
 
   Acc<MODE, NCT> acc;
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
   SmpLane<NCT> sl;
   if constexpr (SMP) smp_lane_init<NCT>(a, lane, sl);
+  // From batch 2 up, the logits of up to HOLD tiles wait in registers and are stored
+  // after the weight stream (measured: storing them tile by tile, in the same in-order
+  // vector-memory queue as the weight stream, cost ~11 us at batch 16 and ~2 us at batch
+  // 4; at batch 1 the per-tile stores are cheaper than the stores at the end, ~0.6 us).
+  constexpr int HOLD = VQK_LM_DEFER > 0 ? VQK_LM_DEFER : 1;
+  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= 2 && my_tiles <= HOLD;
+  uint2 ob[HOLD][NCT];
   uint32_t sdw[16];  // the tile's row-scale dwords (wave-uniform), fetched at its first stage
   int ctile = wid, cks = 0;
 
@@ -1048,7 +1082,20 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
           } else {
             row_scales<MODE>(a, ctile * 16, lane, tsc);  // the ragged last tile
           }
-          epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, SMP ? &sl : nullptr);
+          uint2 nv[NCT];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) nv[ct] = make_uint2(0u, 0u);
+          epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, nv, SMP ? &sl : nullptr);
+          if (hold) {
+#pragma unroll
+            for (int k = 0; k + 1 < HOLD; ++k)
+#pragma unroll
+              for (int ct = 0; ct < NCT; ++ct) ob[k][ct] = ob[k + 1][ct];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) ob[HOLD - 1][ct] = nv[ct];
+          } else {
+            store_tile<NCT>(a, ctile * 16, lane, nv);
+          }
         }
         if (++cks == SPT) {
           cks = 0;
@@ -1058,6 +1105,14 @@ __global__ void __launch_bounds__(256) lmhead_lds_kernel(LmArgs a0) {
     }
   }
   wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
+  if (hold) {
+    // the held logits: tile i of the wave sits in slot HOLD - my_tiles + i
+#pragma unroll
+    for (int k = 0; k < HOLD; ++k) {
+      const int i = k - (HOLD - my_tiles);
+      if (i >= 0) store_tile<NCT>(a, (wid + i * total) * 16, lane, ob[k]);  // wave-uniform test
+    }
+  }
   if constexpr (SMP) {
     // the wave's best key of each batch row: lanes j, j+16, j+32, j+48 hold row j's
 #pragma unroll
