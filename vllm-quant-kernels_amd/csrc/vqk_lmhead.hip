@@ -1026,8 +1026,23 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
   // vector-memory queue as the weight stream, cost ~11 us at batch 16 and ~2 us at batch
   // 4; at batch 1 the per-tile stores are cheaper than the stores at the end, ~0.6 us).
   constexpr int HOLD = VQK_LM_DEFER > 0 ? VQK_LM_DEFER : 1;
-  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= 2 && my_tiles <= HOLD;
+  // With 32 batch columns a wave with more tiles flushes its HOLD held tiles at once
+  // whenever the buffer is full (measured: FP8 / MXFP8 / W8A8 at batch 64, two paired
+  // groups of 31 tiles per wave, 189-204 -> 179-192 us; MXFP4 there, and the 16-column
+  // kernels at batch 4, were slower with the mid-stream flush compiled in).  Held tile k
+  // (of nheld) is the wave's tile hfirst + k - (HOLD - nheld).
+  constexpr bool MIDFLUSH = NCT == 2 && MODE != M_MXFP4;
+  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= 2 && (MIDFLUSH || my_tiles <= HOLD);
   uint2 ob[HOLD][NCT];
+  int nheld = 0, hfirst = 0, wtile = 0;  // wave-uniform
+  auto flush_held = [&]() {
+#pragma unroll
+    for (int k = 0; k < HOLD; ++k) {
+      const int i = hfirst + k - (HOLD - nheld);
+      if (k >= HOLD - nheld) store_tile<NCT>(a, (wid + i * total) * 16, lane, ob[k]);  // wave-uniform test
+    }
+    nheld = 0;
+  };
   uint32_t sdw[16];  // the tile's row-scale dwords (wave-uniform), fetched at its first stage
   int ctile = wid, cks = 0;
 
@@ -1087,15 +1102,19 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
           for (int ct = 0; ct < NCT; ++ct) nv[ct] = make_uint2(0u, 0u);
           epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, nv, SMP ? &sl : nullptr);
           if (hold) {
+            if (MIDFLUSH && nheld == HOLD) flush_held();
 #pragma unroll
             for (int k = 0; k + 1 < HOLD; ++k)
 #pragma unroll
               for (int ct = 0; ct < NCT; ++ct) ob[k][ct] = ob[k + 1][ct];
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) ob[HOLD - 1][ct] = nv[ct];
+            if (nheld == 0) hfirst = wtile;
+            ++nheld;
           } else {
             store_tile<NCT>(a, ctile * 16, lane, nv);
           }
+          ++wtile;
         }
         if (++cks == SPT) {
           cks = 0;
@@ -1105,14 +1124,7 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
     }
   }
   wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
-  if (hold) {
-    // the held logits: tile i of the wave sits in slot HOLD - my_tiles + i
-#pragma unroll
-    for (int k = 0; k < HOLD; ++k) {
-      const int i = k - (HOLD - my_tiles);
-      if (i >= 0) store_tile<NCT>(a, (wid + i * total) * 16, lane, ob[k]);  // wave-uniform test
-    }
-  }
+  if (hold) flush_held();
   if constexpr (SMP) {
     // the wave's best key of each batch row: lanes j, j+16, j+32, j+48 hold row j's
 #pragma unroll
