@@ -57,8 +57,8 @@
 #ifndef VQK_LM_BALANCE
 #define VQK_LM_BALANCE 8   // batch groups up to this size: shrink the grid so every wave
 #endif                     // streams the same number of tiles
-#ifndef VQK_LM_PAIR
-#define VQK_LM_PAIR 1  // two batch groups: one launch of XCD-paired workgroups (1) or two launches (0)
+#ifndef VQK_LM_GROUPS
+#define VQK_LM_GROUPS 4  // batch groups per launch of XCD-grouped workgroups (1: one launch per group)
 #endif
 #ifndef VQK_LM_SC_POLICY
 // cache policy of the MX scale pieces: temporal.  A stage reads 8-16 bytes of each row's
@@ -157,11 +157,11 @@ struct LmArgs {
   int xsr;              // MX: LDS dwords per batch row of activation scales (odd)
   int xs_off;           // MX: LDS byte offset of the activation scales
   int xvec;             // 1 when activation rows (x or xq) allow 16-byte loads
-  // two batch groups in one launch (paired workgroups, see lmhead_lds_kernel): 2, else 1;
-  // the second group's offsets from the first's pointers, and its row count
+  // batch groups in one launch (XCD-grouped workgroups, see lmhead_lds_kernel), else 1;
+  // group g's pointers are group 0's plus g times these strides; the last group's rows
   int ngrp;
-  int64_t g1_x, g1_xq, g1_xsq, g1_out, g1_acc;
-  int g1_Bg;
+  int64_t gs_x, gs_xq, gs_xsq, gs_out, gs_acc;
+  int glast_Bg;
   // fused Gumbel-argmax epilogue (the sampling form only)
   const float* stemp;   // [Bg] temperatures or null (greedy)
   const void* sseeds;   // [Bg] int32 or int64 seeds
@@ -909,10 +909,10 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
   typedef StageGeom<MODE> G;
   constexpr bool T8 = MODE == M_FP8 || MODE == M_MXFP8 || MODE == M_MXFP4;
   const uint8_t* tb = a.w + (int64_t)t * 16 * KB + 256 * ks;  // wave-uniform
-  // One reader per weight line: non-temporal.  Two paired readers (two batch groups) of
-  // the fp8/MX weights: the line stays cached for the second one (measured: MXFP8 B=64
+  // One reader per weight line: non-temporal.  Several grouped readers (batch groups) of
+  // the fp8/MX weights: the line stays cached for the others (measured: MXFP8 B=64
   // 237 -> 204 us; the int8 modes were slower with it, 211 -> 227 us for W8A16 B=32).
-  if (T8 && a.ngrp == 2) {
+  if (T8 && a.ngrp >= 2) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds(VQK_GPTR(tb + o.w[i]), VQK_LPTR(slot + 1024 * i), 16, 0, 0);
@@ -939,24 +939,26 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
   typedef StageGeom<MODE> G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float red[17];
-  // Two batch groups in one launch: workgroups b and b + 8 (the same XCD under the
-  // round-robin dispatch of workgroups to the 8 XCDs) stream the same weight tiles in the
-  // same order for different batch rows, so the second reader of each line finds it in
-  // that XCD's L2 or in the last-level cache: the weight crosses HBM about once instead of
-  // once per group.
+  // G batch groups in one launch: the workgroups of run r of 8 consecutive workgroups
+  // serve group r % G, so workgroups b, b + 8, ..., b + 8(G-1) (the same XCD under the
+  // round-robin dispatch of workgroups to the 8 XCDs) stream the same weight tiles in
+  // the same order for different batch rows, and all but the first reader of each line
+  // find it in that XCD's L2 or in the last-level cache: the weight crosses HBM about
+  // once instead of once per group.
   LmArgs a = a0;
   int bid = blockIdx.x, nwg = gridDim.x;
-  if (a0.ngrp == 2) {
-    const int grp = (bid >> 3) & 1;
-    bid = ((bid >> 4) << 3) | (bid & 7);
-    nwg = gridDim.x >> 1;
+  if (a0.ngrp > 1) {
+    const int G = a0.ngrp, run = bid >> 3;
+    const int grp = run % G;
+    bid = (run / G) * 8 + (bid & 7);
+    nwg = gridDim.x / G;
     if (grp) {
-      a.x = a0.x ? (const void*)((const char*)a0.x + a0.g1_x) : nullptr;
-      a.xq = a0.xq ? a0.xq + a0.g1_xq : nullptr;
-      a.xsq = a0.xsq ? a0.xsq + a0.g1_xsq : nullptr;
-      a.out = a0.out + a0.g1_out;
-      a.acc = a0.acc ? a0.acc + a0.g1_acc : nullptr;
-      a.Bg = a0.g1_Bg;
+      a.x = a0.x ? (const void*)((const char*)a0.x + grp * a0.gs_x) : nullptr;
+      a.xq = a0.xq ? a0.xq + grp * a0.gs_xq : nullptr;
+      a.xsq = a0.xsq ? a0.xsq + grp * a0.gs_xsq : nullptr;
+      a.out = a0.out + grp * a0.gs_out;
+      a.acc = a0.acc ? a0.acc + grp * a0.gs_acc : nullptr;
+      if (grp == G - 1) a.Bg = a0.glast_Bg;
     }
   }
   const int K = a.K;
@@ -1286,7 +1288,9 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   const int ncu = vqk_cu_count();
   const int threads = 512;
 
-  for (int64_t b0 = 0; b0 < B; b0 += gsize) {
+  int64_t adv = gsize;  // batch rows the iteration's launch covered
+  for (int64_t b0 = 0; b0 < B; b0 += adv) {
+    adv = gsize;
     const int Bg = (int)((B - b0) < gsize ? (B - b0) : gsize);
     LmArgs a;
     a.w = w;
@@ -1309,8 +1313,8 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.xs_val = xs_val;
     a.xs_dev = xs_dev;
     a.ngrp = 1;
-    a.g1_x = a.g1_xq = a.g1_xsq = a.g1_out = a.g1_acc = 0;
-    a.g1_Bg = Bg;
+    a.gs_x = a.gs_xq = a.gs_xsq = a.gs_out = a.gs_acc = 0;
+    a.glast_Bg = Bg;
     a.stemp = smp ? smp->temp : nullptr;
     a.sseeds = smp ? smp->seeds : nullptr;
     a.sseed64 = smp ? smp->seed64 : 0;
@@ -1346,30 +1350,33 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       }
       const int nct_l = (Bg + 15) / 16;
       int rcl;
-      if (ngroups == 2 && b0 == 0 && !smp && VQK_LM_PAIR) {
-        // both groups in one launch: half the CUs each, in XCD-aligned runs of 8
+      const int64_t left = (B - b0 + gsize - 1) / gsize;  // batch groups not yet launched
+      const int G = (int)(left < VQK_LM_GROUPS ? left : VQK_LM_GROUPS);
+      if (G >= 2 && !smp) {
+        // G groups in one launch: 1/G of the CUs each, in XCD-aligned runs of 8
         // workgroups; every wave of the launch gets the same number of tiles (+-1)
-        int gpg = (ncu / 2) & ~7;
+        int gpg = (ncu / G) & ~7;
         const int maxg = (((ntiles + 3) / 4) + 7) & ~7;
         if (gpg > maxg) gpg = maxg;
         if (gpg >= 8) {
           const int xes2 = (xdt == VQK_F32) ? 4 : 2;
-          a.ngrp = 2;
-          a.g1_x = (int64_t)gsize * ldx * xes2;
-          a.g1_xq = (int64_t)gsize * K;
-          a.g1_xsq = (int64_t)gsize * (K / 32);
-          a.g1_out = (int64_t)gsize * ldo;
-          a.g1_acc = (int64_t)gsize * M;
-          a.g1_Bg = (int)(B - gsize);
-          const int nct_p = (gsize + 15) / 16;  // the larger group's column tiles
+          a.ngrp = G;
+          a.gs_x = (int64_t)gsize * ldx * xes2;
+          a.gs_xq = (int64_t)gsize * K;
+          a.gs_xsq = (int64_t)gsize * (K / 32);
+          a.gs_out = (int64_t)gsize * ldo;
+          a.gs_acc = (int64_t)gsize * M;
+          a.glast_Bg = (int)(B - b0 - (int64_t)(G - 1) * gsize < gsize ? B - b0 - (int64_t)(G - 1) * gsize : gsize);
+          const int nct_p = (gsize + 15) / 16;  // the larger groups' column tiles
           if constexpr (MODE == M_W8A16) {
-            rcl = launch_lds<MODE, 1>(a, stages, lds_l, 2 * gpg, st);
+            rcl = launch_lds<MODE, 1>(a, stages, lds_l, G * gpg, st);
           } else {
-            rcl = (nct_p == 1) ? launch_lds<MODE, 1>(a, stages, lds_l, 2 * gpg, st)
-                               : launch_lds<MODE, 2>(a, stages, lds_l, 2 * gpg, st);
+            rcl = (nct_p == 1) ? launch_lds<MODE, 1>(a, stages, lds_l, G * gpg, st)
+                               : launch_lds<MODE, 2>(a, stages, lds_l, G * gpg, st);
           }
           if (rcl) return rcl;
-          break;
+          adv = (int64_t)G * gsize;
+          continue;
         }
       }
       if (smp) {
