@@ -79,6 +79,9 @@
 #else
 #define VQK_LM_WPE_ATTR
 #endif
+#ifndef VQK_LM_XU
+#define VQK_LM_XU 4        // activation prologue: 8-element items per thread and round
+#endif
 #ifndef VQK_LM_DEFER
 #define VQK_LM_DEFER 16    // logits held in registers for up to this many tiles per wave
                            // (measured: 32 slows batch 1 by ~1 us); 0: stored tile by tile
@@ -291,7 +294,7 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
       // writes bytes 8(l%2).. of half l/2 of the layout above.
       auto quantize = [&](auto vtag) {
         constexpr bool V = decltype(vtag)::value;
-        constexpr int U = 4;
+        constexpr int U = VQK_LM_XU;
         const int nit = 4 * G * Bg;  // a multiple of 4: a group's lanes share every trip
         for (int i0 = tid; i0 < nit; i0 += U * nth) {
           int f[U], l[U];
@@ -344,7 +347,7 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
     // round with every load issued before the first conversion.
     auto quantize = [&](auto vtag) {
       constexpr bool V = decltype(vtag)::value;
-      constexpr int QU = 4, IPF = T::FB / 8;
+      constexpr int QU = VQK_LM_XU, IPF = T::FB / 8;
       const int nit = nfrag * IPF;
       for (int i0 = tid; i0 < nit; i0 += QU * nth) {
         float xv[QU][8];

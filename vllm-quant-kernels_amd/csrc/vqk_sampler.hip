@@ -40,6 +40,12 @@ namespace vqk {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+#ifndef VQK_CAND_EPT
+#define VQK_CAND_EPT 64  // candidate pass: logits per thread (power of two, >= 8)
+#endif
+#ifndef VQK_SURV_EPT
+#define VQK_SURV_EPT 8   // survivor pass: logits per thread (a multiple of 4)
+#endif
 #ifndef VQK_SURV_LATE
 // survivor pass: request the slice's logits only once it is known to survive (1), or
 // together with the keys (0).  Measured: 1 saves the logit reads of greedy rows and
@@ -647,7 +653,7 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   // scoring.  Larger ones take the candidate and survivor passes.
   const bool small = B * V <= ((int64_t)2 << 20);
   const int64_t max_chunks = gumbel_nchunks(V, SMP_MIN_CHUNK);
-  a.nchunks = (int)gumbel_nchunks(V, small ? SMP_THREADS * 4 : SMP_THREADS * 64);
+  a.nchunks = (int)gumbel_nchunks(V, small ? SMP_THREADS * 4 : SMP_THREADS * VQK_CAND_EPT);
   a.ckeys = (unsigned long long*)workspace;
   a.rkeys = a.ckeys + B * max_chunks;
   a.bkeys = (uint32_t*)(a.rkeys + B);
@@ -656,10 +662,10 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
     hipLaunchKernelGGL(gumbel_local_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                        (hipStream_t)stream, a);
   } else {
-    hipLaunchKernelGGL(gumbel_cand_kernel<64>, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+    hipLaunchKernelGGL(gumbel_cand_kernel<VQK_CAND_EPT>, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                        (hipStream_t)stream, a);
-    const int ns = (int)((V + SMP_THREADS * 8 - 1) / (SMP_THREADS * 8));
-    hipLaunchKernelGGL(gumbel_surv_kernel<8>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+    const int ns = (int)((V + SMP_THREADS * VQK_SURV_EPT - 1) / (SMP_THREADS * VQK_SURV_EPT));
+    hipLaunchKernelGGL(gumbel_surv_kernel<VQK_SURV_EPT>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
   hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
