@@ -49,9 +49,13 @@ def test_sampler_graph_replays_match_eager(B):
     assert torch.equal(out, eager2)
 
 
-@pytest.mark.parametrize("mode", ["w8a16", "w8a8", "fp8", "mxfp8", "mxfp4"])
-def test_lmhead_graph_replays_match_eager(mode):
-    M, K, B = 16384, 3072, 4
+@pytest.mark.parametrize("mode,B", [("w8a16", 4), ("w8a8", 4), ("fp8", 4), ("mxfp8", 4), ("mxfp4", 4),
+                                    ("w8a16", 64), ("fp8", 128), ("mxfp4", 48)])
+def test_lmhead_graph_replays_match_eager(mode, B):
+    """Batch 4: one group, fused activation prologue, held logits; W8A16 64 / FP8 128: four
+    XCD-grouped batch groups in one launch (FP8 after a separate activation cast, 32-row
+    groups flushing held logits); MXFP4 48: two groups of 24."""
+    M, K = 16384, 3072
     g0 = torch.Generator(device="cuda").manual_seed(3)
     w = (torch.randn(M, K, generator=g0, device="cuda") * 0.02).half()
     x = torch.randn(B, K, generator=g0, device="cuda").half()
