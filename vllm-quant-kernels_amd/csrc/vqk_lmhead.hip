@@ -224,7 +224,10 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
   const int nfrag = NMF * 4 * Bg;
 
   float xs_w8a8 = a.xs_val;
-  if (MODE == M_W8A8 && !a.xq) {
+  // W8A8 with the whole activation in this group and at most 8 items per thread: one pass
+  // (load, amax, scale, quantize from registers) instead of an amax pass and a quantize pass
+  const bool w8a8_one = MODE == M_W8A8 && !a.xq && a.Ball == Bg && nfrag * (T::FB / 8) <= 8 * nth;
+  if (MODE == M_W8A8 && !a.xq && !w8a8_one) {
     // per-tensor amax over the whole [Ball, K] activation (bit-exact max, order-free)
     float m = 0.f;
     if (a.xvec) {
@@ -341,6 +344,59 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
       if (a.xvec) quantize(BoolTag<true>{});
       else quantize(BoolTag<false>{});
     }
+  } else if (MODE == M_W8A8 && w8a8_one) {
+    auto one_pass = [&](auto vtag) {
+      constexpr bool V = decltype(vtag)::value;
+      constexpr int QU = 8, IPF = T::FB / 8;
+      const int nit = nfrag * IPF;
+      float xv[QU][8];
+      int fb[QU], fgm[QU], sub[QU];
+      bool ok[QU];
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const int it = tid + u * nth;
+        ok[u] = it < nit;
+        const int ic = ok[u] ? it : nit - 1;
+        const int f = ic / IPF;
+        sub[u] = ic - f * IPF;
+        fb[u] = f % Bg;
+        fgm[u] = f / Bg;
+        const int g = fgm[u] & 3, mi = fgm[u] >> 2;
+        load_run<DT, 8>(a.x, (int64_t)fb[u] * a.ldx + frag_k<MODE>(mi, g, 16 * (sub[u] >> 1)) + 8 * (sub[u] & 1),
+                        V, xv[u]);
+      }
+      // the items cover the activation exactly once; idle slots repeat the last item,
+      // which leaves a maximum unchanged
+      float m = 0.f;
+#pragma unroll
+      for (int u = 0; u < QU; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(xv[u][e]));
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      if ((tid & 63) == 0) lds_red[tid >> 6] = m;
+      __syncthreads();
+      if (tid == 0) {
+        float mm = 0.f;
+        for (int i = 0; i < (nth >> 6); ++i) mm = fmaxf(mm, lds_red[i]);
+        lds_red[16] = fmaxf(mm / 127.0f, 1e-12f);
+      }
+      __syncthreads();
+      const float xs = lds_red[16];
+      const float xi = 1.0f / xs;
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        uint32_t v[2] = {0u, 0u};
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          float q = rint_div_i8(xv[u][p], xs, xi);
+          q = fminf(fmaxf(q, -127.f), 127.f);
+          v[p >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * (p & 3));
+        }
+        if (ok[u]) *(uint2*)(lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB + 8 * sub[u]) = make_uint2(v[0], v[1]);
+      }
+    };
+    if (a.xvec) one_pass(BoolTag<true>{});
+    else one_pass(BoolTag<false>{});
   } else if (MODE != M_W8A16 && !a.xq) {
     // W8A8 (16-element fragments) or FP8 (32): quantize from the exact float, in items of 8
     // consecutive elements (a fragment's runs of 16 split in two), QU items per thread and
