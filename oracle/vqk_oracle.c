@@ -117,6 +117,29 @@ float vqko_gumbel_max_over_all_words(void) {
   return best;
 }
 
+/* The GPU sampler's cheap upper bound of the noise from the exponent of 1 - u (no
+ * counterpart in the reference: it only decides which exact scores the GPU may skip), and
+ * the smallest slack bound - noise over every distinct uniform, walked as above.  A
+ * positive result proves the bound for every Philox word. */
+float vqko_gumbel_upper(float u) {
+  const float t = 1.0f - u;
+  const int e = (int)((bits_from_f32(t) >> 23) & 0xFFu) - 127;
+  return (float)(-e) * 0.693147182f + 0.01f;
+}
+float vqko_gumbel_upper_min_slack(void) {
+  float worst = INFINITY;
+  const float top = 2147483648.0f;
+  float f = 0.0f;
+  for (;;) {
+    const float u = f * 4.6566127342e-10f;
+    const float slack = vqko_gumbel_upper(u) - vqko_gumbel(u);
+    if (slack < worst) worst = slack;
+    if (f >= top) break;
+    f = (f < 16777216.0f) ? f + 1.0f : nextafterf(f, INFINITY);
+  }
+  return worst;
+}
+
 /* Score y of element v (src/vllm_quant_kernels/_sampler_kernels.py:68-113). */
 static float score(float x, int has_t, float T, uint64_t seed, int has_thr, float thr, uint32_t v) {
   if (has_thr && !(x >= thr)) return -INFINITY;

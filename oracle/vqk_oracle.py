@@ -28,6 +28,8 @@ _SIG = {
     "vqko_logf": (_F, [_F]),
     "vqko_gumbel": (_F, [_F]),
     "vqko_gumbel_max_over_all_words": (_F, []),
+    "vqko_gumbel_upper": (_F, [_F]),
+    "vqko_gumbel_upper_min_slack": (_F, []),
     "vqko_gumbel_scores": (None, [_P, _L, _L, _L, _P, _P, _P, _P]),
     "vqko_gumbel_argmax": (None, [_P, _L, _L, _L, _P, _P, _P, _P, _I]),
     "vqko_e4m3_to_f32": (_F, [ctypes.c_uint8]),
@@ -274,3 +276,12 @@ def gumbel_argmax(logits, temp, seeds, thr=None, nthreads: int = 0) -> np.ndarra
 
 def gumbel_max_over_all_words() -> float:
     return float(lib().vqko_gumbel_max_over_all_words())
+
+
+def gumbel_upper(u) -> np.ndarray:
+    u = _f32(u)
+    return np.array([lib().vqko_gumbel_upper(float(x)) for x in u.ravel()], np.float32).reshape(u.shape)
+
+
+def gumbel_upper_min_slack() -> float:
+    return float(lib().vqko_gumbel_upper_min_slack())

@@ -136,6 +136,21 @@ def test_gumbel_range_and_pruning_bound():
     assert abs(g[2] - (-np.log(np.log(2.0)))) < 1e-6
 
 
+def test_gumbel_upper_bound_holds_for_every_word():
+    """The GPU sampler skips the exact score of a logit when x*RN(1/T) + gumbel_upper(u)
+    (+ margins) is below a real element's score; that is exact only if gumbel_upper(u)
+    bounds the computed noise for every Philox word.  Walk every distinct uniform."""
+    slack = O.gumbel_upper_min_slack()
+    assert slack > 0.005, slack               # margin 0.01 minus rounding, never negative
+    u = np.array([0.0, 0.5, 0.75, 1 - 2.0 ** -24, 1 - 2.0 ** -10], np.float32)
+    ub = O.gumbel_upper(u)
+    g = O.gumbel(u)
+    assert np.all(ub >= g)
+    # the bound is tight near u = 1 (where the skip decisions are close calls) and loose
+    # by at most ln 2 + 0.01 + (-log(-log u) vs -log(1-u)) elsewhere
+    assert ub[3] - g[3] < 0.02 and ub[4] - g[4] < 0.7
+
+
 # ---------------------------------------------------------------------------------------
 # number formats
 

@@ -279,6 +279,16 @@ __device__ __forceinline__ float gumbel_from_uniform(float u) {
   return -vqk_logf(-l1);
 }
 
+// An upper bound of gumbel_from_uniform(u) for a Philox uniform u <= 1 - 2^-24 from the
+// exponent of 1 - u alone: -log(-log u) <= -log(1 - u) (as -log u >= 1 - u), and
+// -log t <= -e*ln2 for t = m*2^e, m in [1, 2).  The 0.01 margin covers the rounding of
+// 1 - u and of the exact path (both below 1e-5 here).
+__device__ __forceinline__ float gumbel_upper(float u) {
+  const float t = 1.0f - u;
+  const int e = (int)((bits_f32(t) >> 23) & 0xFFu) - 127;
+  return (float)(-e) * 0.693147182f + 0.01f;
+}
+
 // Order-preserving map float -> uint32 (larger float -> larger key); -0.0 is folded into
 // +0.0 and every NaN into the positive quiet NaN, which orders above +inf (torch.argmax
 // treats NaN as the maximum).

@@ -80,6 +80,7 @@ struct SmpArgs {
 struct RowParams {
   bool greedy;
   float T;
+  float rT;  // RN(1/T), for the prune bound only
   uint32_t k0, k1;
   bool has_thr;
   float thr;
@@ -97,6 +98,7 @@ __device__ __forceinline__ RowParams row_params(const SmpArgs& a, int row) {
   const uint32_t hi = sp[a.seed64 ? 2 * row + 1 : row];
   RowParams p;
   p.T = a.temp ? t : 1.0f;
+  p.rT = 1.0f / p.T;
   p.greedy = a.temp ? (t < GREEDY_EPS) : true;
   p.k0 = lo;
   p.k1 = a.seed64 ? hi : (uint32_t)((int32_t)lo >> 31);  // int32 -> uint64 sign-extends
@@ -118,6 +120,26 @@ __device__ __forceinline__ float score(const RowParams& p, float x, uint32_t v) 
 __device__ __forceinline__ float score_sampled(const RowParams& p, float x, uint32_t v) {
   const float a = x / p.T;
   return a + gumbel_from_uniform(philox_uniform(philox_word0(v, p.k0, p.k1)));
+}
+
+// Fold an admissible, non-NaN logit of a sampled row into a running (best score, index)
+// pair, skipping the exact score when it provably falls below floor or the running best
+// (both scores of real elements, so such a logit cannot be the argmax).  The bound needs
+// only the Philox word: y = x/T + G(u) <= x*RN(1/T) + gumbel_upper(u) + 1e-5*|x*RN(1/T)|
+// (x*RN(1/T) is within 2^-22 relative of x/T; the exact path rounds twice more, each
+// well inside the margins).  Survivors of hot rows sit ~10 below the row's best, where
+// fewer than 1 in 10^4 Philox words come close, so most skip both logarithms and the
+// division.
+__device__ __forceinline__ void score_fold(const RowParams& p, float x, uint32_t v, float floor, float& by,
+                                           uint32_t& bv) {
+  const float u = philox_uniform(philox_word0(v, p.k0, p.k1));
+  const float aq = x * p.rT;
+  const float yub = aq + gumbel_upper(u) + 1e-5f * fabsf(aq);
+  if (yub < fmaxf(floor, by)) return;
+  const float y = x / p.T + gumbel_from_uniform(u);
+  const bool b = (y > by) || (y == by && v < bv);
+  by = b ? y : by;
+  bv = b ? v : bv;
 }
 
 
@@ -490,14 +512,7 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   // stopped above; -0.0 == +0.0 as the order-preserving key has it).
   float by = NEG_INF;
   uint32_t bv = 0xFFFFFFFFu;  // none yet
-  for (int i = tid; i < n; i += SMP_THREADS) {
-    const float x = qx[i];
-    const uint32_t v = qv[i];
-    const float y = score_sampled(p, x, v);
-    const bool b = (y > by) || (y == by && v < bv);
-    by = b ? y : by;
-    bv = b ? v : bv;
-  }
+  for (int i = tid; i < n; i += SMP_THREADS) score_fold(p, qx[i], qv[i], L, by, bv);
   // beating the candidates (score >= L) is rare: only then a wave reduction and an atomic
   if (__ballot(bv != 0xFFFFFFFFu && by >= L)) {
     const unsigned long long gb = wave_max_u64(bv != 0xFFFFFFFFu ? make_key(by, bv) : 0ull);
@@ -565,6 +580,8 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_local_kernel(SmpArgs a) {
     __builtin_amdgcn_wave_barrier();
     float by = NEG_INF;
     uint32_t bv = 0xFFFFFFFFu;
+    // exact scores throughout: a wave's own candidate is a weak floor, so the bound of
+    // score_fold rarely rules a logit out here (measured slower at B = 1 and 4)
     for (int i = lane; i < n; i += 64) {
       const float x = wx[i];
       const uint32_t v = wv[i];
