@@ -1,4 +1,5 @@
-// vqk_sampler.hip - single-launch Gumbel-argmax sampler over [B, V] fp32 logits (gfx950).
+// vqk_sampler.hip - Gumbel-argmax sampler over [B, V] fp32 logits (gfx950), in two or three
+// launches without workspace initialisation.
 //
 // Semantics follow the reference's _gumbel_block_argmax_kernel + host tail
 // (src/vllm_quant_kernels/_sampler_kernels.py:38-182):
@@ -9,7 +10,8 @@
 // G = -log(-log(max(u, 2^-126))) with u = Triton's tl.rand(seed, v): Philox4x32-10 word 0
 // of counter (v, 0, 0, 0) under key (seed lo32, seed hi32).
 //
-// Design (MI355X).  The Philox + two logs cost ~140 VALU instructions per element, so
+// Design (MI355X).  The Philox + two logs + division cost over a hundred VALU instructions
+// per element, so
 // scoring every element of a [32, 248320] batch is ALU-bound (~30 us).  The kernel prunes
 // exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
 // row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
@@ -23,7 +25,9 @@
 //   2. gumbel_surv_kernel re-reads the surviving slices of the sampled rows (recently
 //      streamed, so mostly served by the 256 MB last-level cache), skips slices whose blocks
 //      all lie under the row's cutoff, drops everything else under it with one compare and
-//      scores the survivors through a per-workgroup LDS queue, 64 per wave-step;
+//      scores the survivors through a per-workgroup LDS queue, 64 per wave-step, skipping
+//      the logarithms and the division of those whose Philox word alone bounds them below
+//      a real score (score_fold);
 //   3. gumbel_finish_kernel reduces each row's keys to the token.
 // Smaller batches are a few workgroup latencies long, so launches dominate there: they
 // take gumbel_local_kernel (one pass, each wave pruned against its own best candidate)
