@@ -12,9 +12,9 @@
 //
 // Design (MI355X).  The Philox + two logs + division cost over a hundred VALU instructions
 // per element, so scoring every element of a [32, 248320] batch is ALU-bound (~30 us).
-// The kernels prune
-// exactly instead: the noise is bounded (G <= GUMBEL_MAX for every Philox word), so once a
-// row's winner is known to be >= L, every element with fl(fl(x/T) + GUMBEL_MAX) < L is out.
+// The kernels prune exactly instead: the noise is bounded (G <= GUMBEL_MAX for every
+// Philox word), so once a row's winner is known to be >= L, every element with
+// fl(fl(x/T) + GUMBEL_MAX) < L is out.
 // A good L needs the whole row, so batches of more than ~2M logits take three launches
 // with no spinning, no cross-workgroup waits and no workspace initialisation:
 //   1. gumbel_cand_kernel streams the logits (256 threads x 64 floats per workgroup,
