@@ -251,6 +251,13 @@ int vqk_gumbel_scores(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *temp, const void *seeds, int seed_is_64bit,
                       const float *topk_thr, float *scores, vqk_stream_t stream);
 
+/* Debug, no reference counterpart: over the float32 bit patterns [lo, hi) of magnitude
+ * at most 448 (every pattern if full != 0), add to *count the number whose hardware e4m3
+ * conversion differs from the library's encoder and lower *first to the smallest such
+ * pattern.  *count and *first are device words the caller initialises (0 and 0xFFFFFFFF). */
+int vqk_debug_e4m3_hw_check(uint32_t lo, uint32_t hi, int full, unsigned int *count, unsigned int *first,
+                            vqk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

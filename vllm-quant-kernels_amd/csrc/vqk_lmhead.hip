@@ -323,12 +323,10 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
             const int kx = mx_exponent(amax, 448.0f);
             // x / 2^kx as x * 2^-kx: the same correctly rounded value (2^-kx is exact)
             const float isc = exp2i(-kx);
-            uint32_t v[2] = {0u, 0u};
+            float y[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float y = fminf(fmaxf(xv[u][e] * isc, -448.0f), 448.0f);
-              v[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
-            }
+            for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(xv[u][e] * isc, -448.0f), 448.0f);
+            const uint32_t v[2] = {e4m3x4_clamped(y[0], y[1], y[2], y[3]), e4m3x4_clamped(y[4], y[5], y[6], y[7])};
             if (!ok[u]) continue;
             const int b = f[u] % Bg, grp = f[u] / Bg;
             const int mi = grp >> 2, j = grp & 3;
@@ -425,17 +423,16 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
 #pragma unroll
         for (int u = 0; u < QU; ++u) {
           uint32_t v[2] = {0u, 0u};
+          if constexpr (MODE == M_W8A8) {
 #pragma unroll
-          for (int p = 0; p < 8; ++p) {
-            uint32_t byte;
-            if (MODE == M_W8A8) {
+            for (int p = 0; p < 8; ++p) {
               float q = rint_div_i8(xv[u][p], xs_w8a8, xs_inv);
               q = fminf(fmaxf(q, -127.f), 127.f);
-              byte = (uint32_t)(uint8_t)(int8_t)(int)q;
-            } else {
-              byte = f32_to_e4m3(xv[u][p]);
+              v[p >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)q << (8 * (p & 3));
             }
-            v[p >> 2] |= byte << (8 * (p & 3));
+          } else {
+            v[0] = e4m3x4_torch(xv[u][0], xv[u][1], xv[u][2], xv[u][3]);
+            v[1] = e4m3x4_torch(xv[u][4], xv[u][5], xv[u][6], xv[u][7]);
           }
           if (ok[u]) *(uint2*)(lds + (size_t)fb[u] * a.xr + (size_t)fgm[u] * T::FB + 8 * sub[u]) = make_uint2(v[0], v[1]);
         }

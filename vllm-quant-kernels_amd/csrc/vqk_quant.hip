@@ -95,12 +95,10 @@ __global__ void quant_mx_kernel(const void* t, int64_t R, int64_t K, int64_t ldt
   if (!live) return;
   if (part == 0) scales[row * G + grp] = (uint8_t)(k + 127);
   if (!fp4) {
-    uint32_t w[2] = {0, 0};
+    float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float y = fminf(fmaxf(v[e] * isc, -448.f), 448.f);
-      w[e >> 2] |= (uint32_t)f32_to_e4m3(y) << (8 * (e & 3));
-    }
+    for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(v[e] * isc, -448.f), 448.f);
+    const uint32_t w[2] = {e4m3x4_clamped(y[0], y[1], y[2], y[3]), e4m3x4_clamped(y[4], y[5], y[6], y[7])};
     uint32_t* dst = (uint32_t*)(q + row * K + grp * 32 + part * 8);
     dst[0] = w[0];
     dst[1] = w[1];
@@ -276,5 +274,46 @@ extern "C" int vqk_act_cast_e4m3(const void* x, int x_dtype, int64_t ldx, int64_
   const int64_t n = B * K;
   hipLaunchKernelGGL(act_cast_e4m3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      x, x_dtype, ldx, B, K, xq);
+  return finish();
+}
+
+// ---------------------------------------------------------------------------------------
+// Debug: compare the hardware e4m3 conversions with this library's encoder (f32_to_e4m3,
+// torch's cast semantics) on every float32 bit pattern of [lo, hi): e4m3x4_clamped on the
+// magnitudes up to 448 it is used for, or, with full set, e4m3x4_torch on every pattern
+// (infinities, NaNs and overflow included).
+// Counts mismatches and keeps the smallest mismatching pattern (UINT32_MAX: none).
+__global__ void __launch_bounds__(256) e4m3_hw_check_kernel(uint32_t lo, uint32_t hi, int full,
+                                                            unsigned int* count, unsigned int* first) {
+  unsigned int n = 0, f = 0xFFFFFFFFu;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint64_t b = (uint64_t)lo + blockIdx.x * blockDim.x + threadIdx.x; b < hi; b += stride) {
+    const uint32_t u = (uint32_t)b;
+    if (!full && (u & 0x7FFFFFFFu) > 0x43E00000u) continue;  // |x| > 448 or NaN
+    const float x = __uint_as_float(u);
+    const uint32_t hw = (full ? e4m3x4_torch(x, x, x, x) : e4m3x4_clamped(x, x, x, x)) & 0xFFu;
+    if (hw != f32_to_e4m3(x)) {
+      ++n;
+      f = u < f ? u : f;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    n += __shfl_xor(n, off);
+    const unsigned int o = __shfl_xor(f, off);
+    f = o < f ? o : f;
+  }
+  if ((threadIdx.x & 63) == 0 && n) {
+    atomicAdd(count, n);
+    atomicMin(first, f);
+  }
+}
+
+extern "C" int vqk_debug_e4m3_hw_check(uint32_t lo, uint32_t hi, int full, unsigned int* count,
+                                       unsigned int* first, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  if (!count || !first || hi < lo) return VQK_EINVAL;
+  hipLaunchKernelGGL(e4m3_hw_check_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream, lo, hi, full, count,
+                     first);
   return finish();
 }
