@@ -148,11 +148,15 @@ def _x_for(x, K):
     return x
 
 
-# From this batch size on, the W8A8, e4m3 and MX lm_head wrappers quantize the activations once in
-# a separate launch and run the pre-quantized kernel: the fused form re-quantizes the
-# activations in every workgroup's prologue, which costs more than a launch once the
-# batch is large (measured on MI355X at 248320 x 3072: ~12-18 us at B=16).
-SEPARATE_ACT_QUANT_MIN_B = 8
+# From these batch sizes on, the W8A8, e4m3 and MX lm_head wrappers quantize the activations
+# once in a separate launch and run the pre-quantized kernel: the fused form re-quantizes
+# the activations in every workgroup's prologue, which costs more than a launch once the
+# batch is large.  Crossovers measured on MI355X at 248320 x 3072 (median us per call,
+# fused / separate): W8A8 B=8 123.3 / 121.2; FP8 B=12 121.7 / 123.3, B=16 124.0 / 124.4,
+# B=32 134.1 / 131.5; MXFP8 B=8 118.5 / 119.7, B=12 124.5 / 124.3, B=16 126.5 / 125.5;
+# MXFP4 B=8 66.0 / 67.2, B=12 71.0 / 71.0, B=16 74.0 / 72.2.  Both forms give identical
+# logits.
+SEPARATE_ACT_QUANT_MIN_B = {"w8a8": 8, "fp8": 16, "mxfp8": 12, "mxfp4": 12}
 
 
 def lmhead_w8a16(x, w, s, out=None):
@@ -180,7 +184,7 @@ def lmhead_w8a8(x, w, ws, out=None, acc=None):
     B = x.shape[0]
     if acc is not None:
         assert acc.dtype == torch.int32 and acc.shape == (B, M) and acc.is_contiguous()
-    if B >= SEPARATE_ACT_QUANT_MIN_B:
+    if B >= SEPARATE_ACT_QUANT_MIN_B["w8a8"]:
         xq, xs = act_quant_int8(x)
         return gemm_w8a8_devscale(xq, xs, w, ws, out=out, acc=acc)
     out = _out(out, B, M, x.device)
@@ -197,7 +201,7 @@ def lmhead_fp8(x, w, s, out=None):
     M, K = w.shape
     x = _x_for(x, K)
     B = x.shape[0]
-    if B >= SEPARATE_ACT_QUANT_MIN_B:
+    if B >= SEPARATE_ACT_QUANT_MIN_B["fp8"]:
         return gemm_fp8(act_cast_e4m3(x), w, s, out=out)
     out = _out(out, B, M, x.device)
     _lib.call("vqk_lmhead_fp8", w.data_ptr(), s.data_ptr(), x.data_ptr(), _DT[x.dtype], x.stride(0),
@@ -213,7 +217,7 @@ def lmhead_mxfp8(x, w, ws, out=None):
     M, K = w.shape
     x = _x_for(x, K)
     B = x.shape[0]
-    if B >= SEPARATE_ACT_QUANT_MIN_B:
+    if B >= SEPARATE_ACT_QUANT_MIN_B["mxfp8"]:
         xq, xs = quant_mxfp8(x)
         return gemm_mxfp8(xq, xs, w, ws, out=out)
     out = _out(out, B, M, x.device)
@@ -232,7 +236,7 @@ def lmhead_mxfp4(x, w_packed, ws, K=None, out=None):
     K = int(K) if K is not None else 2 * w_packed.shape[1]
     x = _x_for(x, K)
     B = x.shape[0]
-    if B >= SEPARATE_ACT_QUANT_MIN_B:
+    if B >= SEPARATE_ACT_QUANT_MIN_B["mxfp4"]:
         xq, xs = quant_mxfp8(x)
         return gemm_mxfp4(xq, xs, w_packed, ws, K, out=out)
     out = _out(out, B, M, x.device)
