@@ -1090,7 +1090,12 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
   // kernels at batch 4, were slower with the mid-stream flush compiled in).  Held tile k
   // (of nheld) is the wave's tile hfirst + k - (HOLD - nheld).
   constexpr bool MIDFLUSH = NCT == 2 && MODE != M_MXFP4;
-  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= 2 && (MIDFLUSH || my_tiles <= HOLD);
+  // smallest batch group that holds its logits (per-tile stores are cheaper below it;
+  // medians at 248320 x 3072, held / per tile: MXFP4 B=2 62.0-62.5 / 61.2-61.3 us, B=3
+  // 63.5-63.6 / 62.7-62.9, B=4 equal; MXFP8 B=2 114.7-115.0 / 114.2-114.3; FP8 and W8A8
+  // B=4 114.8-117.5 / 116.3-118.8)
+  constexpr int HOLD_MIN_B = (MODE == M_MXFP4) ? 4 : (MODE == M_MXFP8) ? 3 : 2;
+  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= HOLD_MIN_B && (MIDFLUSH || my_tiles <= HOLD);
   uint2 ob[HOLD][NCT];
   int nheld = 0, hfirst = 0, wtile = 0;  // wave-uniform
   auto flush_held = [&]() {
