@@ -195,7 +195,8 @@ def test_e2m1_vs_bucketize():
     t = torch.from_numpy(y)
     ref = (((t < 0).to(torch.uint8) << 3) | torch.bucketize(t.abs().clamp(max=6.0), mids).to(torch.uint8)).numpy()
     assert np.array_equal(O.e2m1_encode(y), ref)
-    # the survey's probe: ties go to the lower magnitude
+    # values exactly on a midpoint round down (bucketize with right=False): 0.25 -> 0,
+    # 0.75 -> 0.5, 5.0 -> 4, while just above a midpoint rounds up
     assert O.e2m1_encode(np.array([0, .25, .2501, .75, 1.25, 1.75, 2.5, 3.5, 5.0, 5.01, 6], np.float32)).tolist() \
         == [0, 0, 1, 1, 2, 3, 4, 5, 6, 7, 7]
     assert O.e2m1_encode(np.array([-0.0, -1e-6], np.float32)).tolist() == [0, 8]
