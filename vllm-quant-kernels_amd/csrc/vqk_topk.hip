@@ -35,6 +35,7 @@ constexpr int TK_EPW = 4096;         // logits per workgroup in the streaming pa
 constexpr int TK_MAX_NBLK = 4096;    // block maxima per row the select kernel keeps in LDS
 constexpr int TK_CAP = 6144;         // candidate keys collected in LDS
 constexpr int TK_U = 16;             // loads in flight per thread in the candidate scan
+constexpr int TS_THREADS = 1024;     // threads of the per-row select workgroup
 
 __device__ __forceinline__ uint32_t key_at(const float* rowp, int v) { return orderable(rowp[v]); }
 
@@ -92,7 +93,7 @@ __device__ __forceinline__ void pick_digit(const int* hist, int rem, int* sh) {
 }
 
 // Pass 2: one workgroup per row.
-__global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* logits, int64_t ld, int B, int V,
+__global__ void __launch_bounds__(TS_THREADS) topk_select_kernel(const float* logits, int64_t ld, int B, int V,
                                                                  int nblk, int bs, const void* top_k,
                                                                  int topk64, const uint32_t* bmax, float* thr) {
   __shared__ uint32_t sb[TK_MAX_NBLK];     // block maxima of the row
@@ -100,14 +101,14 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
   __shared__ uint32_t ckey[TK_CAP];        // candidate keys (when they fit)
   __shared__ int hist[256];
   __shared__ int sh[4];
-  __shared__ long long smk[TK_THREADS / 64];
+  __shared__ long long smk[TS_THREADS / 64];
   const int row = blockIdx.x, tid = threadIdx.x;
   auto topk_at = [&](int b) -> int64_t {
     return topk64 ? ((const int64_t*)top_k)[b] : (int64_t)((const int32_t*)top_k)[b];
   };
   // the reference's "all rows disabled" test, max over the whole batch
   int64_t mk = INT64_MIN;
-  for (int b = tid; b < B; b += TK_THREADS) {
+  for (int b = tid; b < B; b += TS_THREADS) {
     const int64_t t = topk_at(b);
     mk = t > mk ? t : mk;
   }
@@ -119,7 +120,7 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
   if ((tid & 63) == 0) smk[tid >> 6] = mk;
   __syncthreads();
   mk = smk[0];
-  for (int w = 1; w < TK_THREADS / 64; ++w) mk = mk > smk[w] ? mk : smk[w];
+  for (int w = 1; w < TS_THREADS / 64; ++w) mk = mk > smk[w] ? mk : smk[w];
   if (mk >= (int64_t)V) {
     if (tid == 0) thr[row] = -__builtin_inff();
     return;
@@ -136,24 +137,24 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
   if (fit) {
     {
       // every load issued before any is stored (one memory latency, not one per step)
-      uint32_t t[TK_MAX_NBLK / TK_THREADS];
+      uint32_t t[TK_MAX_NBLK / TS_THREADS];
 #pragma unroll
-      for (int r = 0; r < TK_MAX_NBLK / TK_THREADS; ++r) {
-        const int i = r * TK_THREADS + tid;
+      for (int r = 0; r < TK_MAX_NBLK / TS_THREADS; ++r) {
+        const int i = r * TS_THREADS + tid;
         t[r] = bmax[(int64_t)row * nblk + (i < nblk ? i : nblk - 1)];
       }
 #pragma unroll
-      for (int r = 0; r < TK_MAX_NBLK / TK_THREADS; ++r)
-        if (r * TK_THREADS + tid < nblk) sb[r * TK_THREADS + tid] = t[r];
+      for (int r = 0; r < TK_MAX_NBLK / TS_THREADS; ++r)
+        if (r * TS_THREADS + tid < nblk) sb[r * TS_THREADS + tid] = t[r];
     }
     __syncthreads();
     if (k <= nblk) {
       uint32_t prefix = 0u, mask = 0u;
       int rem = k;
       for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[tid] = 0;
+        if (tid < 256) hist[tid] = 0;
         __syncthreads();
-        for (int i = tid; i < nblk; i += TK_THREADS) {
+        for (int i = tid; i < nblk; i += TS_THREADS) {
           const uint32_t key = sb[i];
           if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
         }
@@ -169,7 +170,7 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
     // the candidate blocks (any order)
     if (tid == 0) sh[2] = 0;
     __syncthreads();
-    for (int i = tid; i < nblk; i += TK_THREADS)
+    for (int i = tid; i < nblk; i += TS_THREADS)
       if (sb[i] >= t0) cblk[atomicAdd(&sh[2], 1)] = i;
     __syncthreads();
     nb = sh[2];
@@ -182,22 +183,22 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
   bool in_lds = false;
   int nkey = 0;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
+    if (tid < 256) hist[tid] = 0;
     if (tid == 0) sh[3] = 0;
     __syncthreads();
     if (in_lds) {
-      for (int i = tid; i < nkey; i += TK_THREADS) {
+      for (int i = tid; i < nkey; i += TS_THREADS) {
         const uint32_t key = ckey[i];
         if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
       }
     } else {
       const bool collect = shift == 24;
-      for (int64_t i0 = 0; i0 < total; i0 += (int64_t)TK_U * TK_THREADS) {
+      for (int64_t i0 = 0; i0 < total; i0 += (int64_t)TK_U * TS_THREADS) {
         // all loads of the step first, then their use
         uint32_t kv[TK_U];
 #pragma unroll
         for (int u = 0; u < TK_U; ++u) {
-          const int64_t i = i0 + u * TK_THREADS + tid;
+          const int64_t i = i0 + u * TS_THREADS + tid;
           int v = V;
           if (i < total) {
             const int j = (int)(i / bs), e = (int)(i - (int64_t)j * bs);
@@ -208,7 +209,7 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(const float* lo
         }
 #pragma unroll
         for (int u = 0; u < TK_U; ++u) {
-          const int64_t i = i0 + u * TK_THREADS + tid;
+          const int64_t i = i0 + u * TS_THREADS + tid;
           const uint32_t key = kv[u];
           const bool c = i < total && key >= t0 && (key & mask) == prefix;
           if (c) atomicAdd(&hist[(key >> shift) & 255], 1);
@@ -274,7 +275,7 @@ extern "C" int vqk_topk_threshold(const float* logits, int64_t ld, int64_t B, in
   else
     hipLaunchKernelGGL(topk_blockmax_kernel<256>, g1, dim3(TK_THREADS), 0, (hipStream_t)stream, logits, ld, (int)V,
                        nblk, vec, bmax);
-  hipLaunchKernelGGL(topk_select_kernel, dim3((unsigned)B), dim3(TK_THREADS), 0, (hipStream_t)stream, logits, ld,
+  hipLaunchKernelGGL(topk_select_kernel, dim3((unsigned)B), dim3(TS_THREADS), 0, (hipStream_t)stream, logits, ld,
                      (int)B, (int)V, nblk, bs, top_k, top_k_is_64bit ? 1 : 0, bmax, thr);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
