@@ -13,9 +13,10 @@
 //   1. topk_blockmax_kernel streams the logits once and stores the largest key of every
 //      block of bs logits (bs = 64 up to V = 256K, 256 up to 1M), so a row has at most 4096
 //      block maxima, which fit LDS.
-//   2. topk_select_kernel, one workgroup per row: t0 = the k-th largest block maximum is a
-//      lower bound of the answer (k distinct logits are >= it) and every logit >= the
-//      answer lies in a block whose maximum is >= t0.  A 4-pass MSB-first 8-bit radix
+//   2. topk_select_kernel, one workgroup per row: t0 = the k-th largest block maximum (for
+//      k <= 256 the lower edge of its 16-bit key bin) is a lower bound of the answer (k
+//      distinct logits are >= that maximum) and every logit >= the answer lies in a block
+//      whose maximum is >= t0.  A 4-pass MSB-first 8-bit radix
 //      select then runs over the keys >= t0 of those blocks only (collected into LDS on the
 //      first pass when they fit, else re-read from memory each pass, 16 loads in flight per
 //      thread).  For k up to the number of blocks that is a few times k keys per row;
@@ -129,8 +130,8 @@ __global__ void __launch_bounds__(TS_THREADS) topk_select_kernel(const float* lo
   const int k = (int)(kk < 1 ? 1 : kk);  // k < V here
   const float* rowp = logits + (int64_t)row * ld;
 
-  // t0: the k-th largest block maximum (0, the smallest key, when k exceeds the blocks or
-  // the row has more blocks than LDS holds)
+  // t0: the k-th largest block maximum or the 16-bit bin edge below it (0, the smallest
+  // key, when k exceeds the blocks or the row has more blocks than LDS holds)
   uint32_t t0 = 0u;
   int nb = nblk;
   const bool fit = nblk <= TK_MAX_NBLK;
@@ -151,7 +152,13 @@ __global__ void __launch_bounds__(TS_THREADS) topk_select_kernel(const float* lo
     if (k <= nblk) {
       uint32_t prefix = 0u, mask = 0u;
       int rem = k;
-      for (int shift = 24; shift >= 0; shift -= 8) {
+      // t0 only has to be a lower bound of the answer: for k <= 256 the lower edge of the
+      // 16-bit key bin that holds the k-th largest block maximum serves (the bin spans 2^-7
+      // of the value, so it adds a few candidate blocks and saves two passes: k = 50
+      // 23.4 -> 21.8 us); larger k, whose candidates are re-read from memory each pass,
+      // take the exact maximum (four passes).
+      const int last = k <= 256 ? 16 : 0;
+      for (int shift = 24; shift >= last; shift -= 8) {
         if (tid < 256) hist[tid] = 0;
         __syncthreads();
         for (int i = tid; i < nblk; i += TS_THREADS) {
