@@ -102,10 +102,10 @@ int vqk_act_cast_e4m3(const void *x, int x_dtype, int64_t ldx, int64_t B, int64_
                       uint8_t *xq, vqk_stream_t stream);
 
 /* lm_head projections: out[b,m] (fp16, [B,M], row stride ldo) -------------------------
- * Shapes handled: K % 128 == 0 (K % 256 == 0 for MXFP4), M >= 1, 0 <= B <= 4096,
- * row stride of every weight matrix = its logical width (contiguous rows).
- * Any B is accepted; batches larger than one launch's LDS budget are split in groups,
- * each of which streams the weight once. */
+ * Shapes handled: K % 128 == 0 (K % 256 == 0 for MXFP4), M >= 1, 0 <= B <= 2^24 with
+ * B * K / 8 < 2^31, row stride of every weight matrix = its logical width (contiguous
+ * rows).  Batches larger than one launch's LDS budget are split in groups of up to 32
+ * rows (W8A16: 16), launched up to four groups at a time. */
 
 /* W8A16: out = fp16( f32(s16[m]) * sum_k f32(w[m,k]) * f32(x[b,k]) ).
  * Replaces: int8_gmv (src/vllm_quant_kernels/_kernels.py:8-84) and int8_gemm (:148-250)
@@ -206,7 +206,8 @@ int vqk_gumbel_argmax(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *topk_thr, int64_t *out, void *workspace,
                       int64_t ws_bytes, vqk_stream_t stream);
 
-/* Fused lm_head + Gumbel-argmax sampling (opt-in; one batch group of B <= 32 rows).
+/* Fused lm_head + Gumbel-argmax sampling (opt-in; one batch group: B <= 32 rows, and
+ * B <= 16 for VQK_MODE_W8A16, else VQK_EUNSUPPORTED).
  * Runs the `mode` projection exactly as vqk_lmhead_<mode> does (same arguments: w, ws,
  * x, x_dtype, ldx, out_f16, ldo, M, K, B; for VQK_MODE_MXFP4, w is the packed [M,K/2] form
  * and K the logical K; W8A16 takes fp16 x only) and, in the same launch's epilogue,
@@ -250,6 +251,14 @@ int vqk_topk_threshold(const float *logits, int64_t ld, int64_t B, int64_t V, co
 int vqk_gumbel_scores(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *temp, const void *seeds, int seed_is_64bit,
                       const float *topk_thr, float *scores, vqk_stream_t stream);
+
+/* Content hash of nbytes of device memory at p (16-byte aligned), for the identity of a
+ * source weight in the on-disk quantized-lm_head cache: out[0], out[1] (device, zero
+ * before the call) receive two 64-bit sums over the buffer's 16-byte chunks, each chunk
+ * mixed with its index (splitmix64), so any changed byte or exchanged pair of chunks
+ * changes both.  One launch; no counterpart in the reference, which re-quantizes on every
+ * load instead of caching (src/vllm_quant_kernels/_quant.py:245-380). */
+int vqk_hash128(const void *p, int64_t nbytes, uint64_t *out, vqk_stream_t stream);
 
 /* Debug, no reference counterpart: over the float32 bit patterns [lo, hi) of magnitude
  * at most 448 (every pattern if full != 0), add to *count the number whose hardware e4m3

@@ -37,8 +37,8 @@ def _plain(mode, x, q, s, K):
     return getattr(K_, "lmhead_" + mode)(x, q, s)
 
 
-@pytest.mark.parametrize("mode", ["w8a16", "w8a8", "fp8", "mxfp8", "mxfp4"])
-@pytest.mark.parametrize("B", [1, 4, 13])
+@pytest.mark.parametrize("mode,B", [(m, b) for m in ("w8a16", "w8a8", "fp8", "mxfp8", "mxfp4")
+                                    for b in (1, 4, 13, 16, 32) if not (m == "w8a16" and b > 16)])
 def test_fused_sample_matches_unfused(mode, B):
     M, K = 20_011, 1024   # ragged M: the last tile is partial
     w = _weights(M, K)
@@ -70,11 +70,14 @@ def test_fused_sample_plain_argmax_and_int32_seeds():
     assert torch.equal(tok, S_.fused_gumbel_sample(logits.float().contiguous(), temp, seeds))
 
 
-def test_fused_sample_rejects_large_batches():
+@pytest.mark.parametrize("mode,B", [("w8a16", 17), ("w8a16", 33), ("fp8", 33), ("mxfp4", 33)])
+def test_fused_sample_rejects_large_batches(mode, B):
+    """One batch group only: 16 rows for W8A16 (fp16 activations take twice the LDS per
+    row), 32 for the other modes."""
     M, K = 4096, 1024
     w = _weights(M, K)
-    q, s = _quantized("w8a16", w)
-    x = torch.randn(33, K, device="cuda").half()
-    seeds = torch.zeros(33, dtype=torch.int32, device="cuda")
-    with pytest.raises(Exception):
-        K_.lmhead_sample("w8a16", x, q, s, None, seeds)
+    q, s = _quantized(mode, w)
+    x = torch.randn(B, K, device="cuda").half()
+    seeds = torch.zeros(B, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError):
+        K_.lmhead_sample(mode, x, q, s, None, seeds, K=K)

@@ -5,9 +5,10 @@ launch writes each workspace value before reading it), so both are capturable.  
 against replay-dependent state, each graph is replayed several times with unrelated eager
 work and synchronizations in between, and every replay is compared with eager execution.
 """
+import numpy as np
 import pytest
 import torch
-
+from oracle import vqk_oracle as O
 from vllm_quant_kernels import _kernels as K_
 from vllm_quant_kernels import _sampler_kernels as S_
 from vllm_quant_kernels import _synthetic as syn
@@ -47,6 +48,34 @@ def test_sampler_graph_replays_match_eager(B):
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, eager2)
+
+
+def test_sampler_graph_survives_larger_call_on_capture_stream():
+    """A larger batch sampled on the capture stream after capture needs a larger workspace;
+    the one the graph captured must stay allocated (and zero at rest) for its replays."""
+    logits, temp, seeds = syn.sampler_inputs(4, 50_000)
+    eager = S_.fused_gumbel_sample(logits, temp, seeds).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        S_.fused_gumbel_sample(logits, temp, seeds)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = S_.fused_gumbel_sample(logits, temp, seeds)
+    big, btemp, bseeds = syn.sampler_inputs(64)
+    with torch.cuda.stream(s):
+        tok_big = S_.fused_gumbel_sample(big, btemp, bseeds)
+        junk = torch.full((1 << 22,), 7, dtype=torch.uint8, device="cuda")  # reuses freed blocks
+    torch.cuda.synchronize()
+    ref_big = O.gumbel_argmax(big.cpu().numpy(), btemp.cpu().numpy(), bseeds.cpu().numpy())
+    assert np.array_equal(tok_big.cpu().numpy(), ref_big)
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+    del junk
 
 
 @pytest.mark.parametrize("mode,B", [("w8a16", 4), ("w8a8", 4), ("fp8", 4), ("mxfp8", 4), ("mxfp4", 4),

@@ -8,7 +8,7 @@ import torch
 from oracle import vqk_oracle as O
 from vllm_quant_kernels import _sampler_kernels as S_
 from vllm_quant_kernels import _synthetic as syn
-from vllm_quant_kernels._sampler import _compute_topk_threshold
+from oracle.torch_chains import compute_topk_threshold as _compute_topk_threshold
 
 pytestmark = pytest.mark.gpu
 

@@ -271,7 +271,7 @@ def test_greedy_and_fallbacks_on_host(fused_cls):
 
 
 def test_topk_threshold_host():
-    from vllm_quant_kernels._sampler import _compute_topk_threshold
+    from oracle.torch_chains import compute_topk_threshold as _compute_topk_threshold
     torch.manual_seed(0)
     logits = torch.randn(3, 50)
     k = torch.tensor([1, 5, 50], dtype=torch.int32)
@@ -364,6 +364,25 @@ def test_quantized_checkpoint_round_trip(tmp_path, mode):
     wrong = "int8" if mode != "int8" else "fp8"
     assert C.load_quantized(fresh, path, mode=wrong) is None
     assert C.load_quantized(fresh, str(tmp_path / "missing.safetensors")) is None
+
+
+def test_quantized_checkpoint_fingerprint_covers_every_row(tmp_path):
+    """A weight that differs from the cached one in a single element of any row (here rows
+    a sampling fingerprint would skip: 1 and M // 2 + 1) must not load the stale file."""
+    from vllm_quant_kernels import _checkpoint as C
+    M, K = 1000, 64
+    head, _ = _fake_head(M, K)
+    head._int8_w = torch.zeros(M, K, dtype=torch.int8)
+    head._int8_scales = torch.ones(M, dtype=torch.float16)
+    path = str(tmp_path / "lm.safetensors")
+    C.save_quantized(head, path)
+    for row in (1, M // 2 + 1, M - 2):
+        other, _ = _fake_head(M, K)
+        other.weight.data[row, 7] += 1.0
+        assert C.fingerprint(other.weight.data) != C.fingerprint(head.weight.data)
+        assert C.load_quantized(other, path) is None, row
+    same, _ = _fake_head(M, K)
+    assert C.load_quantized(same, path) == "int8"
 
 
 def test_quantized_checkpoint_rejects_foreign_files(tmp_path):

@@ -1,28 +1,34 @@
 // vqk_lmhead.hip - quantized lm_head projections for gfx950 (MI355X), all five modes.
 //
 // out[b, m] = epilogue_m( sum_k W[m, k] * X[b, k] ) for a [M, K] quantized weight that is
-// streamed from HBM exactly once per launch.  One kernel template serves every mode and
-// every batch size; the work is shaped for CDNA4 rather than for a warp-GEMV:
+// streamed from HBM exactly once per launch (per launch of up to four batch groups).  One
+// kernel template serves every mode and batch size; the work is shaped for CDNA4 rather
+// than for a warp-GEMV:
 //
-//  * Each wavefront owns 16-row tiles of W.  Lane l holds row (l % 16) and k-block (l / 16)
-//    of the MFMA A operand, which is exactly the 16x16xKB MFMA register layout, so the
-//    weights go from a global_load_dwordx4 straight into the matrix core (int8 and e4m3/
-//    E2M1 need no conversion; W8A16 converts int8 -> fp16 with a byte permute and one
-//    packed fp16 add).  The batch (1..32 rows) is the MFMA N dimension, zero-padded to 16;
-//    at batch 1 the matrix core is 1/16 busy, which still leaves it far faster than HBM.
-//  * Because the reduction over k is order-free, a lane may hold any k positions as long
-//    as the B operand (activations) holds the same ones.  The loads are laid out so that
-//    the four k-block lanes of a row read 64 (or 128) contiguous bytes per instruction,
-//    and the activations are staged once per workgroup in LDS in the matching "fragment"
-//    order, so each B operand is one conflict-free ds_read_b128 (or two).
-//  * MX modes use the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4: a lane's 32 k values
-//    are one 32-element MX group, so the per-lane scale operand is simply that group's
-//    E8M0 byte (weights) and the activation group's byte (from LDS).
-//  * Workgroups are persistent (a few per CU); each wave walks its tiles as one flat
-//    sequence of 128-byte-per-row chunks through a D-deep register ring, so loads for the
-//    next tile are in flight while the current tile's epilogue runs.
-//  * Runtime activation quantization (per-tensor INT8, e4m3 cast, MXFP8) runs in every
-//    workgroup's prologue while it stages X into LDS; no extra launch, no host sync.
+//  * Hot path, lmhead_lds_kernel: persistent 256-thread workgroups (one per CU, two for
+//    W8A16 at small batches).  Each wave owns 16-row tiles and streams them through a
+//    ring of 2-4 LDS stages per wave: a stage is 256 bytes of each of the tile's 16 rows,
+//    fetched by global_load_lds DMA (16 lanes x 16 bytes per row, contiguous, rotated by
+//    16 bytes per row so the MFMA-layout ds_read_b128s that follow are conflict-free),
+//    with the stage's MX scale bytes riding the same DMA.  One s_waitcnt covers a stage.
+//  * MFMA per mode, A = 16 weight rows, B = 16 batch columns (zero-padded; one column
+//    tile per 16 batch rows): W8A16 v_mfma_f32_16x16x32_f16 after an exact int8 -> fp16
+//    byte permute; W8A8 v_mfma_i32_16x16x64_i8; FP8 and MXFP8
+//    v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3, E8M0 scales per 32-k group straight into
+//    the instruction; 127 = 1.0 for FP8); MXFP4 the same instruction with E2M1 weights.
+//    A lane's 32 k values of the scaled forms are exactly one MX group.
+//  * Activations are staged once per workgroup in LDS in MFMA-fragment order by the
+//    prologue, fused with the runtime activation quantization (per-tensor INT8, e4m3
+//    cast, MXFP8), so every B operand is an immediate-offset ds_read_b128; large batches
+//    quantize once in a separate launch instead.
+//  * The epilogue applies the reference's per-row scale order and either stores each
+//    tile's fp16 logits (batch 1) or holds them in registers until the weight stream ends
+//    (a store burst then, instead of stores queued behind the weight loads).
+//  * Batches beyond one group's LDS budget run up to four XCD-grouped batch groups in one
+//    launch, so the later readers of each weight line find it in L2 or the last-level cache.
+//  * Fallback, lmhead_kernel: when K or the scale alignment rules out 256-byte stages, a
+//    512-thread kernel keeps a D-deep ring of 128-byte chunks per lane in registers; same
+//    prologue, MFMA and epilogue code.
 //
 // Reference semantics: src/vllm_quant_kernels/_kernels.py (int8_gmv :8-84, int8_gemm
 // :148-250, fp8_gemm :258-360, int8_w8a8_gemm :369-479, mxfp8_gemm :491-634, mxfp4_gemm
@@ -35,65 +41,29 @@
 #include "vqk_internal.h"
 #include "vqk_math.h"
 
-// Build-time tuning knobs (defaults are the measured choice).
-#ifndef VQK_LM_NT
-#define VQK_LM_NT 0        // 1: non-temporal weight loads (measured slower on MI355X)
-#endif
-#ifndef VQK_LM_WG_PER_CU
-#define VQK_LM_WG_PER_CU 2 // persistent workgroups per CU when the LDS footprint allows
-#endif
-#ifndef VQK_LM_DEPTH
-#define VQK_LM_DEPTH 4     // largest register-ring depth (chunks in flight per wave)
-#endif
-#ifndef VQK_LM_LDS
-#define VQK_LM_LDS 1       // stage weights through LDS with direct-to-LDS loads when K allows
-#endif
-#ifndef VQK_LM_LDS_STAGES
-#define VQK_LM_LDS_STAGES 4  // LDS ring depth per wave (4 KB stages) when LDS allows, else 2
-#endif
-#ifndef VQK_LM_LDS_WG_PER_CU
-#define VQK_LM_LDS_WG_PER_CU 1
-#endif
-#ifndef VQK_LM_BALANCE
-#define VQK_LM_BALANCE 8   // batch groups up to this size: shrink the grid so every wave
-#endif                     // streams the same number of tiles
-#ifndef VQK_LM_GROUPS
-#define VQK_LM_GROUPS 4  // batch groups per launch of XCD-grouped workgroups (1: one launch per group)
-#endif
-#ifndef VQK_LM_SC_POLICY
-// cache policy of the MX scale pieces: temporal.  A stage reads 8-16 bytes of each row's
-// scale line and the following stages read the rest of that line, so the line must stay in
-// L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
-#define VQK_LM_SC_POLICY 0
-#endif
-#ifndef VQK_LM_WPE
-// >0: amdgpu_waves_per_eu(1, VQK_LM_WPE) on the LDS-staged kernel.  Its LDS footprint
-// allows one workgroup (one wave per SIMD) per CU, so the compiler may spend registers
-// on keeping LDS reads in flight instead of aiming for an occupancy that cannot occur
-// (measured: without it the W8A16 loop waits on every fragment read once the held logits
-// take their registers, 113 -> 131 us at batch 1).
-#define VQK_LM_WPE 2
-#endif
-#if VQK_LM_WPE > 0
-#define VQK_LM_WPE_ATTR __attribute__((amdgpu_waves_per_eu(1, VQK_LM_WPE)))
-#else
-#define VQK_LM_WPE_ATTR
-#endif
-#ifndef VQK_LM_XU
-#define VQK_LM_XU 4        // activation prologue: 8-element items per thread and round
-#endif
-#ifndef VQK_LM_DEFER
-#define VQK_LM_DEFER 16    // logits held in registers for up to this many tiles per wave
-                           // (measured: 32 slows batch 1 by ~1 us); 0: stored tile by tile
-#endif
-#ifndef VQK_LM_NT_LDS
-#define VQK_LM_NT_LDS 2    // cache-policy bits of global_load_lds: 2 = non-temporal
-#endif
-#if VQK_LM_NT
-#define VQK_LOAD(p) __builtin_nontemporal_load(p)
-#else
-#define VQK_LOAD(p) (*(p))
-#endif
+namespace vqk {
+
+// Measured choices (MI355X, 248320 x 3072):
+// - activation prologue: 8-element items per thread and round;
+constexpr int LM_XU = 4;
+// - logits held in registers for up to this many tiles per wave before a store burst
+//   (32 slows batch 1 by ~1 us);
+constexpr int LM_HOLD_TILES = 16;
+// - register-ring kernel: up to two persistent workgroups per CU;
+constexpr int LM_RING_WG_PER_CU = 2;
+// - batch groups up to this size shrink the grid so every wave streams the same number
+//   of tiles;
+constexpr int LM_BALANCE_MAX_B = 8;
+// - batch groups per launch of XCD-grouped workgroups;
+constexpr int LM_MAX_GROUPS = 4;
+// - cache policy of the weight DMA: non-temporal (one reader per line);
+constexpr int LM_W_POLICY = 2;
+// - cache policy of the MX scale pieces: temporal.  A stage reads 8-16 bytes of each row's
+//   scale line and the following stages read the rest of that line, so the line must stay
+//   in L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
+constexpr int LM_S_POLICY = 0;
+
+}  // namespace vqk
 
 namespace vqk {
 
@@ -297,7 +267,7 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
       // writes bytes 8(l%2).. of half l/2 of the layout above.
       auto quantize = [&](auto vtag) {
         constexpr bool V = decltype(vtag)::value;
-        constexpr int U = VQK_LM_XU;
+        constexpr int U = LM_XU;
         const int nit = 4 * G * Bg;  // a multiple of 4: a group's lanes share every trip
         for (int i0 = tid; i0 < nit; i0 += U * nth) {
           int f[U], l[U];
@@ -401,7 +371,7 @@ __device__ __forceinline__ void stage_x_dt(const LmArgs& a, uint8_t* lds, uint32
     // round with every load issued before the first conversion.
     auto quantize = [&](auto vtag) {
       constexpr bool V = decltype(vtag)::value;
-      constexpr int QU = VQK_LM_XU, IPF = T::FB / 8;
+      constexpr int QU = LM_XU, IPF = T::FB / 8;
       const int nit = nfrag * IPF;
       for (int i0 = tid; i0 < nit; i0 += QU * nth) {
         float xv[QU][8];
@@ -545,8 +515,8 @@ struct Slot<M_MXFP8> {
 template <int MODE>
 __device__ __forceinline__ void load_chunk(Slot<MODE>& s, const uint8_t* rowp, const uint32_t* srowp,
                                            int c, int g) {
-  v4i lo = VQK_LOAD((const v4i*)(rowp + 128 * c + 16 * g));
-  v4i hi = VQK_LOAD((const v4i*)(rowp + 128 * c + 64 + 16 * g));
+  v4i lo = *(const v4i*)(rowp + 128 * c + 16 * g);
+  v4i hi = *(const v4i*)(rowp + 128 * c + 64 + 16 * g);
   if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
     s.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   } else {
@@ -975,22 +945,26 @@ __device__ __forceinline__ void issue_stage(const LmArgs& a, int KB, int t, int 
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(VQK_GPTR(tb + o.w[i]), VQK_LPTR(slot + 1024 * i), 16, 0, VQK_LM_NT_LDS);
+      __builtin_amdgcn_global_load_lds(VQK_GPTR(tb + o.w[i]), VQK_LPTR(slot + 1024 * i), 16, 0, LM_W_POLICY);
   }
   if constexpr (G::SB > 0) {
     const uint8_t* sb = (const uint8_t*)a.ws + (int64_t)t * 16 * (a.K >> 5) + G::SB * ks;
     if (MODE == M_MXFP8) {
       if (lane < 32)
-        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 4, 0, VQK_LM_SC_POLICY);
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 4, 0, LM_S_POLICY);
     } else {
       if (lane < 16)
-        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 16, 0, VQK_LM_SC_POLICY);
+        __builtin_amdgcn_global_load_lds(VQK_GPTR(sb + o.s), VQK_LPTR(slot + LDS_STAGE), 16, 0, LM_S_POLICY);
     }
   }
 }
 
+// Its LDS footprint allows one or two workgroups (one or two waves per SIMD) per CU, so
+// the compiler may spend registers on keeping LDS reads in flight instead of aiming for an
+// occupancy that cannot occur (without the hint the W8A16 loop waited on every fragment
+// read once the held logits took their registers: 113 -> 131 us at batch 1).
 template <int MODE, int NCT, int S, bool SMP = false>
-__global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs a0) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) lmhead_lds_kernel(LmArgs a0) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1083,7 +1057,7 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
   // after the weight stream (measured: storing them tile by tile, in the same in-order
   // vector-memory queue as the weight stream, cost ~11 us at batch 16 and ~2 us at batch
   // 4; at batch 1 the per-tile stores are cheaper than the stores at the end, ~0.6 us).
-  constexpr int HOLD = VQK_LM_DEFER > 0 ? VQK_LM_DEFER : 1;
+  constexpr int HOLD = LM_HOLD_TILES;
   // With 32 batch columns a wave with more tiles flushes its HOLD held tiles at once
   // whenever the buffer is full (measured: FP8 / MXFP8 / W8A8 at batch 64, two paired
   // groups of 31 tiles per wave, 189-204 -> 179-192 us; MXFP4 there, and the 16-column
@@ -1095,7 +1069,7 @@ __global__ void __launch_bounds__(256) VQK_LM_WPE_ATTR lmhead_lds_kernel(LmArgs 
   // 63.5-63.6 / 62.7-62.9, B=4 equal; MXFP8 B=2 114.7-115.0 / 114.2-114.3; FP8 and W8A8
   // B=4 114.8-117.5 / 116.3-118.8)
   constexpr int HOLD_MIN_B = (MODE == M_MXFP4) ? 4 : (MODE == M_MXFP8) ? 3 : 2;
-  const bool hold = VQK_LM_DEFER > 0 && a.out_vec && a.Bg >= HOLD_MIN_B && (MIDFLUSH || my_tiles <= HOLD);
+  const bool hold = a.out_vec && a.Bg >= HOLD_MIN_B && (MIDFLUSH || my_tiles <= HOLD);
   uint2 ob[HOLD][NCT];
   int nheld = 0, hfirst = 0, wtile = 0;  // wave-uniform
   auto flush_held = [&]() {
@@ -1225,9 +1199,8 @@ __global__ void __launch_bounds__(256) lmhead_sample_finish_kernel(const unsigne
 
 // ---------------------------------------------------------------------------------------
 // Host side
+// register-ring depth (chunks in flight per wave); 6 and 8 measured no faster than 4
 static int pick_depth(int cpr) {
-  if (VQK_LM_DEPTH >= 8 && cpr % 8 == 0) return 8;
-  if (VQK_LM_DEPTH >= 6 && cpr % 6 == 0) return 6;
   if (cpr % 4 == 0) return 4;
   if (cpr % 2 == 0) return 2;
   return 1;
@@ -1242,12 +1215,6 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
     hipLaunchKernelGGL((lmhead_kernel<MODE, NCT, DD>), dim3(grid), dim3(threads), lds_bytes, st, a); \
     break;
     VQK_L(1) VQK_L(2) VQK_L(4)
-#if VQK_LM_DEPTH >= 6
-    VQK_L(6)
-#endif
-#if VQK_LM_DEPTH >= 8
-    VQK_L(8)
-#endif
 #undef VQK_L
     default:
       return VQK_EINVAL;
@@ -1258,15 +1225,8 @@ static int launch_nct(const LmArgs& a, int depth, size_t lds_bytes, int grid, in
 
 template <int MODE, int NCT, bool SMP = false>
 static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, hipStream_t st) {
-  // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute
-#if VQK_LM_LDS_STAGES >= 6
-  // deeper rings (measured: no faster than 4 stages on MI355X, so not built by default)
-  if (stages == 8)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 8, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
-  else if (stages == 6)
-    hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 6, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
-  else
-#endif
+  // gfx950 grants up to 160 KB of dynamic LDS per workgroup without an opt-in attribute;
+  // rings of 6 and 8 stages measured no faster than 4
   if (stages == 4)
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 4, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else if (stages == 3)
@@ -1325,7 +1285,11 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   if (M < 1 || K < 1 || B < 0 || (x && ldx < K) || ldo < M) return VQK_EINVAL;
   if (B == 0) return VQK_OK;
   const int64_t kmult = (MODE == M_MXFP4) ? 256 : 128;
-  if (K % kmult != 0 || M > (int64_t)INT32_MAX - 16 || K > (1 << 20) || B > 4096) return VQK_EUNSUPPORTED;
+  // B is unbounded in practice (batch groups are launched in turn); the fused W8A8 prologue
+  // indexes the whole [B, K/8] activation with 32-bit integers
+  if (K % kmult != 0 || M > (int64_t)INT32_MAX - 16 || K > (1 << 20) || B > (1 << 24) ||
+      B * (K / 8) > (int64_t)INT32_MAX)
+    return VQK_EUNSUPPORTED;
   if (((uintptr_t)w & 15) != 0) return VQK_EUNSUPPORTED;
 
   const int KB = (int)((MODE == M_MXFP4) ? K / 2 : K);
@@ -1335,7 +1299,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
   const size_t lds_cap = 150 * 1024;
   // The LDS-staged kernel needs whole 256-byte stages and 16-byte aligned scale rows; it
   // reserves 4 waves x 2 stages of ring next to the activations.
-  const bool lds_path = VQK_LM_LDS && KB % 256 == 0 && ((uintptr_t)ws & 15) == 0;
+  const bool lds_path = KB % 256 == 0 && ((uintptr_t)ws & 15) == 0;
   const size_t ring2 = (size_t)4 * 2 * G::SLOT;
   // batch group size: up to 16*NCT rows, limited by LDS
   int gmax = (int)(((lds_path ? lds_cap - ring2 : lds_cap) - 64) / xl.per_row());
@@ -1393,17 +1357,26 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     a.lds_x_bytes = (int)lds;
     const int ntiles = (int)((M + 15) / 16);
     if (lds_path && lds + ring2 <= lds_cap) {
-      // the deepest ring (8, 6, 4, 3 or 2 stages per wave) that fits next to the activations
-      auto fits = [&](int n) { return VQK_LM_LDS_STAGES >= n && lds + (size_t)4 * n * G::SLOT <= lds_cap; };
-      const int stages = fits(8) ? 8 : fits(6) ? 6 : fits(4) ? 4 : fits(3) ? 3 : 2;
+      // The deepest ring (4, 3 or 2 stages per wave) that fits next to the activations.
+      // W8A16 prefers two workgroups per CU (two waves per SIMD) with a shallower ring when
+      // both fit in the CU's 160 KB: its int8 -> fp16 conversion and four MFMAs per 128
+      // bytes make one wave per SIMD issue-bound whenever the shader clock dips (measured
+      // at batch 1 while the clock settles after a burst begins, 1.5-1.9 GHz: 135-158 us
+      // with one workgroup per CU, 117-122 us with two); the other modes stream at the HBM
+      // rate with one.
+      auto fits = [&](int n, int per_cu) {
+        return (size_t)per_cu * (lds + (size_t)4 * n * G::SLOT + 512) <= (per_cu == 1 ? lds_cap : 160 * 1024);
+      };
+      int per_cu_l = 1, stages = 0;
+      if (MODE == M_W8A16 && !smp)
+        for (int n = 4; n >= 2 && !stages; --n)
+          if (fits(n, 2)) stages = n, per_cu_l = 2;
+      if (!stages) stages = fits(4, 1) ? 4 : fits(3, 1) ? 3 : 2;
       const size_t lds_l = lds + (size_t)4 * stages * G::SLOT;
-      int per_cu_l = (int)(lds_cap / (lds_l + 512));
-      if (per_cu_l > VQK_LM_LDS_WG_PER_CU) per_cu_l = VQK_LM_LDS_WG_PER_CU;
-      if (per_cu_l < 1) per_cu_l = 1;
       int grid_l = ncu * per_cu_l;
       const int max_grid_l = (ntiles + 3) / 4;
       if (grid_l > max_grid_l) grid_l = max_grid_l;
-      if (Bg <= VQK_LM_BALANCE) {
+      if (Bg <= LM_BALANCE_MAX_B) {
         // as few waves as still give every wave the same (maximal) number of tiles, so
         // the stream keeps all of them busy to the end
         const int tpw = (ntiles + 4 * grid_l - 1) / (4 * grid_l);
@@ -1412,7 +1385,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       const int nct_l = (Bg + 15) / 16;
       int rcl;
       const int64_t left = (B - b0 + gsize - 1) / gsize;  // batch groups not yet launched
-      const int G = (int)(left < VQK_LM_GROUPS ? left : VQK_LM_GROUPS);
+      const int G = (int)(left < LM_MAX_GROUPS ? left : LM_MAX_GROUPS);
       if (G >= 2 && !smp) {
         // G groups in one launch: 1/G of the CUs each, in XCD-aligned runs of 8
         // workgroups; every wave of the launch gets the same number of tiles (+-1)
@@ -1466,7 +1439,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     }
     if (smp) return VQK_EUNSUPPORTED;  // the sampling form needs the LDS kernel
     int per_cu = (int)((150 * 1024) / (lds + 1024));
-    if (per_cu > VQK_LM_WG_PER_CU) per_cu = VQK_LM_WG_PER_CU;
+    if (per_cu > LM_RING_WG_PER_CU) per_cu = LM_RING_WG_PER_CU;
     if (per_cu < 1) per_cu = 1;
     int grid = ncu * per_cu;
     const int max_grid = (ntiles + (threads / 64) - 1) / (threads / 64);

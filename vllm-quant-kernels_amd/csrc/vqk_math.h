@@ -125,18 +125,10 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float x) {
 // Four floats of magnitude at most 448 -> their e4m3fn bytes (a in the low byte), by the
 // hardware conversion: on that range it equals f32_to_e4m3 for every float32 (checked
 // exhaustively on the GPU by vqk_debug_e4m3_hw_check).  Callers clamp first.
-#ifndef VQK_E4M3_HW
-#define VQK_E4M3_HW 1  // 0: the software encoder in the MX quantizers as well
-#endif
 __device__ __forceinline__ uint32_t e4m3x4_clamped(float a, float b, float c, float d) {
-#if VQK_E4M3_HW
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
-#else
-  return f32_to_e4m3(a) | ((uint32_t)f32_to_e4m3(b) << 8) | ((uint32_t)f32_to_e4m3(c) << 16) |
-         ((uint32_t)f32_to_e4m3(d) << 24);
-#endif
 }
 
 // The same for any floats with torch's float8_e4m3fn cast semantics (no clamp: overflow
@@ -144,7 +136,6 @@ __device__ __forceinline__ uint32_t e4m3x4_clamped(float a, float b, float c, fl
 // f32_to_e4m3 on every float32 except positive NaNs, which are set here (checked
 // exhaustively by vqk_debug_e4m3_hw_check with full set).
 __device__ __forceinline__ uint32_t e4m3x4_torch(float a, float b, float c, float d) {
-#if VQK_E4M3_HW
   uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
   const float v[4] = {a, b, c, d};
@@ -155,10 +146,6 @@ __device__ __forceinline__ uint32_t e4m3x4_torch(float a, float b, float c, floa
     if ((bi & 0x7FFFFFFFu) > 0x7F800000u) w = (w & ~(0xFFu << (8 * i))) | (code << (8 * i));
   }
   return w;
-#else
-  return f32_to_e4m3(a) | ((uint32_t)f32_to_e4m3(b) << 8) | ((uint32_t)f32_to_e4m3(c) << 16) |
-         ((uint32_t)f32_to_e4m3(d) << 24);
-#endif
 }
 
 // e4m3fn byte -> float (exact).

@@ -44,18 +44,11 @@ namespace vqk {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-#ifndef VQK_CAND_EPT
-#define VQK_CAND_EPT 64  // candidate pass: logits per thread (power of two, >= 8)
-#endif
-#ifndef VQK_SURV_EPT
-#define VQK_SURV_EPT 8   // survivor pass: logits per thread (a multiple of 4)
-#endif
-#ifndef VQK_SURV_LATE
-// survivor pass: request the slice's logits only once it is known to survive (1), or
-// together with the keys (0).  Measured: 1 saves the logit reads of greedy rows and
-// skipped slices (B=32 24.3 -> 23.8 us, all-greedy B=128 45.7 -> 32.3 us).
-#define VQK_SURV_LATE 1
-#endif
+// candidate pass: logits per thread (a power of two >= 8; 32 measured within noise, 128 does
+// not fit the block-max butterfly's registers); survivor pass: logits per thread (4 and 16
+// measured 0.7-6 us slower)
+constexpr int SMP_CAND_EPT = 64;
+constexpr int SMP_SURV_EPT = 8;
 constexpr int SMP_THREADS = 256;
 // candidate pass: 64 elements per thread (16 for small batches, which gives more, shorter
 // workgroups); its smallest chunk bounds the number of candidate slots per row
@@ -457,7 +450,6 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
       for (int q = 0; q < EPT; ++q) xv[q] = rowp[min(slice_v(base, tid, q), a.V - 1)];
     }
   };
-  if (!VQK_SURV_LATE) load_logits();
   const RowParams p = row_params(a, row);
   if (p.greedy) return;
   const float NEG_INF = -__builtin_inff();
@@ -479,7 +471,9 @@ __global__ void __launch_bounds__(SMP_THREADS) gumbel_surv_kernel(SmpArgs a) {
   }
   __syncthreads();
   if (!sgo) return;
-  if (VQK_SURV_LATE) load_logits();
+  // the logits only now: greedy rows and skipped slices never read them (B=32 24.3 ->
+  // 23.8 us, all-greedy B=128 45.7 -> 32.3 us against requesting them with the keys)
+  load_logits();
   const float xc = sxc, L = sL;
   // Survivors of the whole workgroup go to one LDS queue: each wave counts its survivors
   // of every step (ballots), reserves its run with one LDS atomic and writes them in
@@ -674,7 +668,7 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   // scoring.  Larger ones take the candidate and survivor passes.
   const bool small = B * V <= ((int64_t)2 << 20);
   const int64_t max_chunks = gumbel_nchunks(V, SMP_MIN_CHUNK);
-  a.nchunks = (int)gumbel_nchunks(V, small ? SMP_THREADS * 4 : SMP_THREADS * VQK_CAND_EPT);
+  a.nchunks = (int)gumbel_nchunks(V, small ? SMP_THREADS * 4 : SMP_THREADS * SMP_CAND_EPT);
   a.ckeys = (unsigned long long*)workspace;
   a.rkeys = a.ckeys + B * max_chunks;
   a.bkeys = (uint32_t*)(a.rkeys + B);
@@ -683,10 +677,10 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
     hipLaunchKernelGGL(gumbel_local_kernel, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                        (hipStream_t)stream, a);
   } else {
-    hipLaunchKernelGGL(gumbel_cand_kernel<VQK_CAND_EPT>, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
+    hipLaunchKernelGGL(gumbel_cand_kernel<SMP_CAND_EPT>, dim3(a.nchunks, (unsigned)B), dim3(SMP_THREADS), 0,
                        (hipStream_t)stream, a);
-    const int ns = (int)((V + SMP_THREADS * VQK_SURV_EPT - 1) / (SMP_THREADS * VQK_SURV_EPT));
-    hipLaunchKernelGGL(gumbel_surv_kernel<VQK_SURV_EPT>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
+    const int ns = (int)((V + SMP_THREADS * SMP_SURV_EPT - 1) / (SMP_THREADS * SMP_SURV_EPT));
+    hipLaunchKernelGGL(gumbel_surv_kernel<SMP_SURV_EPT>, dim3(ns, (unsigned)B), dim3(SMP_THREADS), 0, (hipStream_t)stream, a);
   }
   hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();

@@ -250,7 +250,8 @@ _SAMPLE_MODES = {"w8a16": 0, "w8a8": 1, "fp8": 2, "mxfp8": 3, "mxfp4": 4}
 
 
 def lmhead_sample(mode: str, x, w, ws, temperature, seeds, K=None, out=None):
-    """Fused lm_head + Gumbel-argmax sampling (opt-in, B <= 32): returns (tokens int64 [B],
+    """Fused lm_head + Gumbel-argmax sampling (opt-in, one batch group: B <= 32, and
+    B <= 16 for W8A16; larger batches raise ValueError): returns (tokens int64 [B],
     logits fp16 [B,M]).  The tokens equal those of lmhead_<mode> followed by
     fused_gumbel_sample(logits.float(), temperature, seeds) bit for bit; the sampling runs
     in the projection's epilogue, so the logits are not re-read.  No top-k."""
@@ -263,6 +264,9 @@ def lmhead_sample(mode: str, x, w, ws, temperature, seeds, K=None, out=None):
     if mode == "w8a16" and x.dtype != torch.float16:
         x = x.to(torch.float16)
     B = x.shape[0]
+    if B > (16 if mode == "w8a16" else 32):
+        raise ValueError(f"lmhead_sample: batch {B} exceeds one batch group of the {mode} kernel "
+                         f"({16 if mode == 'w8a16' else 32} rows)")
     assert seeds.shape == (B,) and seeds.dtype in (torch.int32, torch.int64)
     seeds = seeds.contiguous()
     if temperature is not None:
@@ -372,12 +376,20 @@ def _view(ptr_t, rows, cols, stride_r):
 
 
 def _int8_gmv(out, w, x, s, M, K, stride_ob, stride_xb, NUM_BATCH=1, **_):
-    """int8_gmv (src/vllm_quant_kernels/_kernels.py:8-84): out[b, :M] for b < NUM_BATCH."""
+    """int8_gmv (src/vllm_quant_kernels/_kernels.py:8-84): out[b, :M] for b < NUM_BATCH.
+    The reference kernel loads x in whatever float dtype it has; the HIP kernel reads fp16,
+    so bf16/fp32 activations are converted first (as _int8_gemm does).  out must be fp16."""
     B = int(NUM_BATCH)
     xv = _view(x, B, K, stride_xb)
     ov = _view(out, B, M, stride_ob)
     _dev(xv, w, s, ov)
-    _lib.call("vqk_lmhead_w8a16", w.data_ptr(), s.data_ptr(), xv.data_ptr(), stride_xb, ov.data_ptr(),
+    if out.dtype != torch.float16:
+        raise ValueError(f"int8_gmv: out must be float16, got {out.dtype}")
+    if xv.dtype not in _DT:
+        raise ValueError(f"int8_gmv: unsupported activation dtype {xv.dtype}")
+    if xv.dtype != torch.float16:
+        xv = xv.to(torch.float16)
+    _lib.call("vqk_lmhead_w8a16", w.data_ptr(), s.data_ptr(), xv.data_ptr(), xv.stride(0), ov.data_ptr(),
               stride_ob, M, K, B, _stream(w))
 
 

@@ -3,12 +3,12 @@
 Behaviour follows the reference hook (src/vllm_quant_kernels/_sampler.py:28-214): only
 ``Sampler.sample`` is overridden; anything outside the fused fast path (top-p, allowed-token
 masks, bad words, logits processors, thinking budgets, per-request generators, processed
-logprobs) is handed to the upstream implementation unchanged.  The fast path itself is one
-HIP launch (``fused_gumbel_sample``).
+logprobs) is handed to the upstream implementation unchanged.  The fast path runs on the
+device with no host synchronisation: the top-k threshold (``topk_threshold``, when top-k is
+on) and the Gumbel-argmax (``fused_gumbel_sample``).
 """
 from __future__ import annotations
 
-import os
 import sys
 from typing import TYPE_CHECKING
 
@@ -39,17 +39,6 @@ def _fast_path_ok(sampling_metadata: "SamplingMetadata") -> bool:
     if sm.generators:
         return False
     return True
-
-
-def _compute_topk_threshold(logits: torch.Tensor, top_k: torch.Tensor, vocab_size: int):
-    """Per-row k-th largest raw logit, or None when top-k is off for every row
-    (reference src/vllm_quant_kernels/_sampler.py:62-93)."""
-    max_k = int(top_k.max().item())
-    if max_k >= vocab_size:
-        return None
-    vals, _ = torch.topk(logits, max_k, dim=-1, sorted=True)
-    col = (top_k.clamp(max=max_k) - 1).clamp(min=0).to(torch.int64).unsqueeze(-1)
-    return vals.gather(dim=-1, index=col).squeeze(-1).contiguous()
 
 
 def _make_seeds(batch_size: int, device: torch.device) -> torch.Tensor:
@@ -87,7 +76,8 @@ def install_fused_sampler() -> None:
             B, V = logits.shape
             thr = None
             if sm.top_k is not None:
-                # on the device, no host sync; equal in effect to _compute_topk_threshold
+                # on the device, no host sync; equal in effect to the reference's
+                # _compute_topk_threshold (src/vllm_quant_kernels/_sampler.py:62-93)
                 thr = topk_threshold(logits, sm.top_k)
             seeds = _make_seeds(B, logits.device)
             sampled = fused_gumbel_sample(
@@ -104,9 +94,3 @@ def install_fused_sampler() -> None:
     print("[vllm-quant-kernels] FusedSampler installed (vllm.v1.sample.sampler.Sampler patched).",
           file=sys.stderr, flush=True)
 
-
-def env_bool(name: str, default: bool = False) -> bool:
-    val = os.environ.get(name, "")
-    if val == "":
-        return default
-    return val.lower() in ("1", "true", "yes", "on")

@@ -1,9 +1,13 @@
-"""Fused Gumbel-argmax sampling over [B, V] fp32 logits (three short HIP launches).
+"""Fused Gumbel-argmax sampling over [B, V] fp32 logits (two or three short HIP launches).
 
 Replaces the reference's Triton block-argmax kernel plus its two-op host tail
 (src/vllm_quant_kernels/_sampler_kernels.py:38-182) with ``vqk_gumbel_argmax``: the
 temperature scaling, Philox noise, top-k masking, per-slice argmax and the cross-slice
-reduction all happen inside one kernel that reads the logits once.
+reduction all happen on the device without a host synchronisation.  Up to ~2M logits one
+launch scores each workgroup's slice against its own best candidate and a second reduces
+the workgroups' keys to the tokens; larger batches stream the logits once to find every
+row's candidates and block maxima, re-read only the slices that can still hold the winner
+(mostly from the last-level cache) and then reduce.
 
 Per row b and vocab index v the kernel takes the argmax (smallest index on ties) of
   y = x                                  if temperature is None or temperature[b] < 1e-5,
@@ -29,15 +33,16 @@ _workspaces: dict = {}
 def _workspace(device: torch.device, stream: int, B: int, V: int) -> torch.Tensor:
     """Per (device, stream) workspace, grown as needed.  The kernels write every value
     before reading it, so it needs no initialisation.  Launches on one stream are ordered,
-    so sharing it among them is safe; different streams get different workspaces."""
+    so sharing it among them is safe; different streams get different workspaces.  A
+    workspace outgrown by a larger batch is kept alive rather than freed: a HIP graph
+    captured earlier on that stream may still replay into it."""
     need = int(_lib.load().vqk_gumbel_workspace_size(B, V))
     key = (device.index, stream)
     with _ws_lock:
-        ws = _workspaces.get(key)
-        if ws is None or ws.numel() < need:
-            ws = torch.empty(max(need, 4096), dtype=torch.uint8, device=device)
-            _workspaces[key] = ws
-    return ws
+        held = _workspaces.setdefault(key, [])
+        if not held or held[-1].numel() < need:
+            held.append(torch.empty(max(need, 4096), dtype=torch.uint8, device=device))
+        return held[-1]
 
 
 def fused_gumbel_sample(
