@@ -206,6 +206,19 @@ int vqk_gumbel_argmax(const float *logits, int64_t ld, int64_t B, int64_t V,
                       const float *topk_thr, int64_t *out, void *workspace,
                       int64_t ws_bytes, vqk_stream_t stream);
 
+/* vqk_gumbel_argmax without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture that may not hipMalloc, tight serving loops,
+ * harnesses that forbid allocation).  It has no counterpart in the reference.  The
+ * workspace is a static device array of vqk_gumbel_noalloc_max_bytes() = 1 MiB that the
+ * library holds on each GPU it runs on until the process ends (at V = 248320, B <= 358
+ * rows fit); larger calls return VQK_EWORKSPACE.  Calls that overlap on one GPU share the
+ * array and race: issue them on one stream.  Same arguments and results as
+ * vqk_gumbel_argmax minus the workspace; no allocation, no memset. */
+int64_t vqk_gumbel_noalloc_max_bytes(void);
+int vqk_gumbel_argmax_noalloc(const float *logits, int64_t ld, int64_t B, int64_t V,
+                              const float *temp, const void *seeds, int seed_is_64bit,
+                              const float *topk_thr, int64_t *out, vqk_stream_t stream);
+
 /* Fused lm_head + Gumbel-argmax sampling (opt-in; one batch group: B <= 32 rows, and
  * B <= 16 for VQK_MODE_W8A16, else VQK_EUNSUPPORTED).
  * Runs the `mode` projection exactly as vqk_lmhead_<mode> does (same arguments: w, ws,

@@ -36,6 +36,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "vqk.h"
 #include "vqk_internal.h"
 #include "vqk_math.h"
@@ -641,17 +643,11 @@ static int smp_check(const float* logits, int64_t ld, int64_t B, int64_t V, cons
   return VQK_OK;
 }
 
-extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int64_t V, const float* temp,
-                                 const void* seeds, int seed_is_64bit, const float* topk_thr, int64_t* out,
-                                 void* workspace, int64_t ws_bytes, vqk_stream_t stream) {
-  int rc = vqk_device_check();
-  if (rc) return rc;
-  rc = smp_check(logits, ld, B, V, seeds);
-  if (rc) return rc;
-  if (!out || !workspace) return VQK_EINVAL;
-  if (B == 0) return VQK_OK;
-  if (ws_bytes < vqk_gumbel_workspace_size(B, V)) return VQK_EWORKSPACE;
-  if (((uintptr_t)workspace & 7) != 0) return VQK_EINVAL;
+// Enqueues the sampler's launches with `workspace` (checked by the callers: at least
+// vqk_gumbel_workspace_size(B, V) bytes, 8-byte aligned, device memory).
+static int gumbel_launch(const float* logits, int64_t ld, int64_t B, int64_t V, const float* temp,
+                         const void* seeds, int seed_is_64bit, const float* topk_thr, int64_t* out,
+                         void* workspace, vqk_stream_t stream) {
   SmpArgs a = {};
   a.logits = logits;
   a.ld = ld;
@@ -685,6 +681,69 @@ extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int
   hipLaunchKernelGGL(gumbel_finish_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
+}
+
+extern "C" int vqk_gumbel_argmax(const float* logits, int64_t ld, int64_t B, int64_t V, const float* temp,
+                                 const void* seeds, int seed_is_64bit, const float* topk_thr, int64_t* out,
+                                 void* workspace, int64_t ws_bytes, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  rc = smp_check(logits, ld, B, V, seeds);
+  if (rc) return rc;
+  if (!out || !workspace) return VQK_EINVAL;
+  if (B == 0) return VQK_OK;
+  if (ws_bytes < vqk_gumbel_workspace_size(B, V)) return VQK_EWORKSPACE;
+  if (((uintptr_t)workspace & 7) != 0) return VQK_EINVAL;
+  return gumbel_launch(logits, ld, B, V, temp, seeds, seed_is_64bit, topk_thr, out, workspace, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free form: the workspace is this file's own device array.  Every GPU the
+// library runs on holds one copy until the process ends; host code must use the address
+// hipGetSymbolAddress returns for the current device (the array's name on the host is
+// only a stand-in), resolved once per device on the first call there.  The sampler writes
+// every workspace value before reading it, so nothing needs clearing between calls; calls
+// that overlap on one GPU (two streams at once) share the array and race.
+constexpr int64_t SMP_STATIC_BYTES = 1 << 20;
+static __device__ __align__(256) unsigned char scratch[SMP_STATIC_BYTES];
+
+namespace {
+constexpr int kMaxScratchDev = 64;
+void* g_scratch[kMaxScratchDev];
+std::mutex g_scratch_mu;
+}  // namespace
+
+static int scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDev) return VQK_ENODEVICE;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return VQK_ENODEVICE;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return VQK_OK;
+}
+
+extern "C" int64_t vqk_gumbel_noalloc_max_bytes(void) { return SMP_STATIC_BYTES; }
+
+extern "C" int vqk_gumbel_argmax_noalloc(const float* logits, int64_t ld, int64_t B, int64_t V, const float* temp,
+                                         const void* seeds, int seed_is_64bit, const float* topk_thr,
+                                         int64_t* out, vqk_stream_t stream) {
+  int rc = vqk_device_check();
+  if (rc) return rc;
+  rc = smp_check(logits, ld, B, V, seeds);
+  if (rc) return rc;
+  if (!out) return VQK_EINVAL;
+  if (B == 0) return VQK_OK;
+  if (vqk_gumbel_workspace_size(B, V) > SMP_STATIC_BYTES) return VQK_EWORKSPACE;
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc) return rc;
+  return gumbel_launch(logits, ld, B, V, temp, seeds, seed_is_64bit, topk_thr, out, ws, stream);
 }
 
 extern "C" int vqk_gumbel_scores(const float* logits, int64_t ld, int64_t B, int64_t V, const float* temp,

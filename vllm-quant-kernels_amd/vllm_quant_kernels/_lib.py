@@ -58,6 +58,8 @@ SIGNATURES = {
     "vqk_gumbel_workspace_size": (_L, [_L, _L]),
     "vqk_gumbel_argmax": (_I, [_P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _L, _P]),
     "vqk_gumbel_scores": (_I, [_P, _L, _L, _L, _P, _P, _I, _P, _P, _P]),
+    "vqk_gumbel_noalloc_max_bytes": (_L, []),
+    "vqk_gumbel_argmax_noalloc": (_I, [_P, _L, _L, _L, _P, _P, _I, _P, _P, _P]),
     "vqk_debug_e4m3_hw_check": (_I, [ctypes.c_uint32, ctypes.c_uint32, _I, _P, _P, _P]),
     "vqk_hash128": (_I, [_P, _L, _P, _P]),
 }
