@@ -369,3 +369,20 @@ def test_sampler_temperature_scaling(T):
     emp = np.mean(out == np.argmax(logits))
     theo = float(torch.softmax(torch.from_numpy(logits) / T, 0).max())
     assert abs(emp - theo) < 3 * np.sqrt(theo * (1 - theo) / N) + 0.01
+
+
+def test_numpy_sampler_baseline_matches_oracle():
+    """The host timing baseline of the sampler (numpy) gives the C oracle's tokens on
+    config-5 style rows: greedy rows, temperatures 0.3-1.5, spikes, a top-k threshold."""
+    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(3)
+    B, V = 12, 20_000
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    for b in range(B):
+        x[b, rng.choice(V, 5, replace=False)] += 10 + 10 * rng.random(5).astype(np.float32)
+    t = (0.3 + 1.2 * rng.random(B)).astype(np.float32)
+    t[[1, 6]] = 0.0
+    seeds = rng.integers(-(2 ** 63), 2 ** 63 - 1, B, dtype=np.int64)
+    assert np.array_equal(CB.gumbel_argmax_numpy(x, t, seeds), O.gumbel_argmax(x, t, seeds))
+    thr = np.sort(x, axis=1)[:, -50].copy()
+    assert np.array_equal(CB.gumbel_argmax_numpy(x, t, seeds, thr), O.gumbel_argmax(x, t, seeds, thr))
