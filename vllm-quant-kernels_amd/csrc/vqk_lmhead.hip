@@ -62,6 +62,9 @@ constexpr int LM_W_POLICY = 2;
 //   scale line and the following stages read the rest of that line, so the line must stay
 //   in L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
 constexpr int LM_S_POLICY = 0;
+// - wide-batch kernel: weight ring stages per wave, and the smallest batch it serves;
+constexpr int LM_WIDE_STAGES = 8;
+constexpr int LM_WIDE_MIN_B = 33;
 
 }  // namespace vqk
 
@@ -183,6 +186,10 @@ __device__ __forceinline__ void smp_lane_init(const LmArgs& a, int lane, SmpLane
 template <bool B_>
 struct BoolTag {
   static constexpr bool value = B_;
+};
+template <int V_>
+struct IntTag {
+  static constexpr int value = V_;
 };
 
 template <int MODE, int DT>
@@ -1178,6 +1185,283 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Wide-batch variant (33-64 batch rows in one pass over the weight).  With the activations
+// of a 64-row batch in LDS there is no room for a weight ring (192 KB at K = 3072), and two
+// 32-row groups stream every weight line through each CU twice while the activation
+// fragments are re-read from LDS for every weight chunk (measured at FP8 batch 64: LDS
+// traffic ~3x the weight bytes, 6-7x the bank conflicts of batch 1, MFMA busy 11%).
+// Here the NW waves of a workgroup split K instead of rows: wave w owns bytes
+// [w * SPW * 256, (w + 1) * SPW * 256) of every weight row and keeps the MFMA B fragments
+// of its slice of all batch columns in VGPRs for the whole launch, so LDS holds only the
+// weight ring (S stages per wave) and the accumulator hand-off.
+// The waves form a pipeline over the workgroup's tiles: in step s wave w works on tile
+// s - w, starting from the accumulators wave w - 1 left in LDS in step s - 1, and the last
+// wave applies the epilogue.  Every tile's MFMA chain therefore runs over K in the same
+// order as in lmhead_lds_kernel, so each batch row's logits are bit-identical to the same
+// row computed in any other batch.  The weight stream runs ahead of the pipeline: every
+// wave's ring is filled at the start, so the wave that starts computing NW - 1 steps late
+// finds its stages landed.
+template <int MODE>
+struct FragT {
+  typedef v8i type;  // 32-byte B fragments of the 16x16x128 f8f6f4 MFMA
+};
+template <>
+struct FragT<M_W8A8> {
+  typedef v4i type;
+};
+template <>
+struct FragT<M_W8A16> {
+  typedef v8h type;
+};
+template <int MODE, int NCT, int NMW>
+struct XRegs {
+  typename FragT<MODE>::type f[NCT][NMW];
+  uint32_t sb[NCT][NMW];  // MX: the fragment's E8M0 byte in bits 0..7
+};
+
+// Copies this wave's fragments (MFMAs mi0 .. mi0 + NMW - 1 of every row) of the column tiles
+// held by staged half h (batch rows 32h .. 32h + bh - 1) from the prologue's LDS layout into
+// registers.  Columns past Bg repeat row Bg - 1, as in x_pointers().
+template <int MODE, int NCT, int NMW>
+__device__ __forceinline__ void load_xregs(XRegs<MODE, NCT, NMW>& xr, const LmArgs& a, const uint8_t* lds,
+                                           const uint32_t* lxs, int h, int mi0, int g, int j) {
+  typedef ModeTraits<MODE> T;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    if (ct / 2 != h) continue;
+    const int b = min(ct * 16 + j, a.Bg - 1) - 32 * h;
+    const uint8_t* xb = lds + b * a.xr + g * T::FB;
+#pragma unroll
+    for (int ml = 0; ml < NMW; ++ml) {
+      const int mi = mi0 + ml;
+      const v4i* p = (const v4i*)(xb + mi * 4 * T::FB);
+      if constexpr (T::FB == 32) {
+        const v4i b0 = p[0], b1 = p[1];
+        xr.f[ct][ml] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+        xr.f[ct][ml] = __builtin_bit_cast(typename FragT<MODE>::type, p[0]);
+      }
+      if constexpr (T::MX) xr.sb[ct][ml] = lxs[b * a.xsr + (mi >> 2) * 4 + g] >> (8 * (mi & 3));
+    }
+  }
+}
+
+// compute_chunk() with the B fragments of the wave's local chunk cl taken from registers.
+template <int MODE, int NCT, int NMW>
+__device__ __forceinline__ void compute_chunk_reg(Acc<MODE, NCT>& acc, const Slot<MODE>& s, int cl, int g,
+                                                  const XRegs<MODE, NCT, NMW>& xr) {
+  if constexpr (MODE == M_W8A16) {
+    uint32_t d[8] = {(uint32_t)s.lo.x, (uint32_t)s.lo.y, (uint32_t)s.lo.z, (uint32_t)s.lo.w,
+                     (uint32_t)s.hi.x, (uint32_t)s.hi.y, (uint32_t)s.hi.z, (uint32_t)s.hi.w};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      v2h p0, p1, p2, p3;
+      i8x4_to_h(d[2 * m], p0, p1);
+      i8x4_to_h(d[2 * m + 1], p2, p3);
+      v8h A = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc.v[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, xr.f[ct][4 * cl + m], acc.v[ct], 0, 0, 0);
+    }
+  } else if constexpr (MODE == M_W8A8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const v4i A = h ? s.hi : s.lo;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc.v[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, xr.f[ct][2 * cl + h], acc.v[ct], 0, 0, 0);
+    }
+  } else if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
+    const int sa = (MODE == M_MXFP8) ? (int)(s.s0 >> (8 * g)) : 127;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int sb = (MODE == M_MXFP8) ? (int)xr.sb[ct][cl] : 127;
+      acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s.w, xr.f[ct][cl], acc.v[ct], 0, 0, 0, sa, 0, sb);
+    }
+  } else {  // MXFP4
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const v4i w = h ? s.hi : s.lo;
+      const v8i A = __builtin_shufflevector(w, w, 0, 1, 2, 3, -1, -1, -1, -1);
+      const int sa = (int)((h ? s.s1 : s.s0) >> (8 * g));
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc.v[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, xr.f[ct][2 * cl + h], acc.v[ct], 4, 0, 0,
+                                                                     sa, 0, (int)xr.sb[ct][2 * cl + h]);
+    }
+  }
+}
+
+template <int MODE, int NCT, int NW, int SPW, int S>
+__global__ void __launch_bounds__(64 * (NW + 1)) __attribute__((amdgpu_waves_per_eu(1, 1)))
+lmhead_wide_kernel(LmArgs a) {
+  typedef ModeTraits<MODE> T;
+  typedef StageGeom<MODE> G;
+  typedef typename AccT<MODE>::type AccV;
+  constexpr int NMW = 2 * SPW * T::MPC;  // MFMAs per column tile of a wave's slice of a row
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ float red[17];
+  const int K = a.K;
+  const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // NW = the writer
+  const int r = lane & 15, g = lane >> 4;
+  const int ntiles = (a.M + 15) >> 4;
+  const int bid = blockIdx.x, nwg = gridDim.x;
+  // a contiguous range of tiles per workgroup (>= 1 tile: the grid has at most ntiles
+  // workgroups), so the four tiles whose logits share a 128-byte line of an output row
+  // are written from one CU
+  const int tpw = ntiles / nwg, trem = ntiles % nwg;
+  const int my_tiles = tpw + (bid < trem ? 1 : 0);
+  const int t0 = bid * tpw + min(bid, trem);
+
+  // Prologue: the activations in halves of up to 32 batch rows through the shared staging
+  // code (which also quantizes them), each compute wave keeping its fragments in registers.
+  XRegs<MODE, NCT, NMW> xr;
+  float xs_w8a8 = 0.f;
+  // (one pass per half, written out so the column tiles a pass fills are compile-time)
+  auto stage_half = [&](auto htag) {
+    constexpr int h = decltype(htag)::value;
+    LmArgs ah = a;
+    ah.Bg = min(32, a.Bg - 32 * h);
+    if (h) {
+      const int xes = (a.xdt == VQK_F32) ? 4 : 2;
+      if (a.x) ah.x = (const void*)((const char*)a.x + (int64_t)32 * h * a.ldx * xes);
+      if (a.xq) ah.xq = a.xq + (int64_t)32 * h * K;
+      if (a.xsq) ah.xsq = a.xsq + (int64_t)32 * h * (K >> 5);
+    }
+    ah.xs_off = ah.Bg * a.xr;
+    const uint32_t* lxs = (const uint32_t*)(smem + ah.xs_off);
+    stage_x<MODE>(ah, smem, (uint32_t*)lxs, red);
+    if (MODE == M_W8A8 && h == 0) xs_w8a8 = red[16];
+    ah.Bg = a.Bg;  // load_xregs clamps against the whole group
+    if (wave < NW) load_xregs<MODE, NCT, NMW>(xr, ah, smem, lxs, h, wave * NMW, g, r);
+    __syncthreads();
+  };
+  stage_half(IntTag<0>{});
+  if constexpr (NCT > 2) stage_half(IntTag<1>{});
+
+  // LDS: the compute waves' rings, then the accumulator hand-off [2][NW][NCT][64 lanes]:
+  // slot w of a step holds compute wave w's accumulators (slot NW - 1: the finished tile).
+  AccV* hand = (AccV*)(smem + NW * S * G::SLOT);
+  const int nsteps = my_tiles + NW;
+  if (wave == NW) {
+    // The writer: dequantizes and stores each finished tile one step after the last
+    // compute wave handed it over.  It issues no weight loads, so no stage wait ever waits
+    // for a store (stores and loads retire in order through one counter).
+    uint32_t sdw[16];
+    for (int s = 0; s < nsteps; ++s) {
+      const int i = s - NW;
+      if (i >= 0) {
+        const int ctile = t0 + i;
+        const bool tile_full = ctile * 16 + 16 <= a.M;
+        if (T::ROWSCALE && tile_full) tile_scales_smem<MODE>(a, ctile, sdw);
+        Acc<MODE, NCT> acc;
+        const AccV* hp = hand + (((s - 1) & 1) * NW + NW - 1) * NCT * 64 + lane;
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) acc.v[ct] = hp[ct * 64];
+        float tsc[4];
+        if (!T::ROWSCALE) {
+          tsc[0] = tsc[1] = tsc[2] = tsc[3] = 1.f;
+        } else if (tile_full) {
+          uint32_t raw[4];
+          select_tile_scales<MODE>(sdw, g, raw);
+          row_scales_from_bits<MODE>(a, ctile * 16, lane, raw, tsc);
+        } else {
+          row_scales<MODE>(a, ctile * 16, lane, tsc);
+        }
+        uint2 nv[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) nv[ct] = make_uint2(0u, 0u);
+        epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, nv, nullptr);
+        store_tile<NCT>(a, ctile * 16, lane, nv);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    return;
+  }
+
+  uint8_t* ring = smem + wave * (S * G::SLOT);
+  IssueOffsets<MODE> io;
+  const int nst = my_tiles * SPW;
+  int itile = t0, iks = 0, iq = 0;
+  issue_offsets<MODE>(a, KB, itile, lane, io);
+  auto issue_next = [&](uint8_t* slot) {
+    issue_stage<MODE>(a, KB, itile, wave * SPW + iks, slot, lane, io);
+    ++iq;
+    if (++iks == SPW) {
+      iks = 0;
+      itile += 1;
+      if (iq < nst) issue_offsets<MODE>(a, KB, itile, lane, io);
+    }
+  };
+#pragma unroll
+  for (int s0 = 0; s0 < S; ++s0)
+    if (iq < nst) issue_next(ring + s0 * G::SLOT);
+
+  const uint32_t rbase = (uint32_t)((r >> 2) * 1024 + (r & 3) * 256);
+  uint32_t wpo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wpo[i] = rbase + ((64 * i + 16 * g + 16 * r) & 255);
+  const uint32_t spo = LDS_STAGE + G::SB * r;
+
+  int q = 0, slot = 0;
+  for (int s = 0; s < nsteps; ++s) {
+    const int i = s - wave;  // wave-uniform
+    if (i >= 0 && i < my_tiles) {
+      Acc<MODE, NCT> acc;
+      if (wave == 0) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) acc.zero(ct);
+      } else {
+        const AccV* hp = hand + (((s - 1) & 1) * NW + wave - 1) * NCT * 64 + lane;
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) acc.v[ct] = hp[ct * 64];
+      }
+#pragma unroll
+      for (int ks = 0; ks < SPW; ++ks) {
+        if (iq == q + S) wait_vmcnt<(S - 1) * G::NV>();
+        else wait_vmcnt<0>();
+        const uint8_t* sp = ring + slot * G::SLOT;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          Slot<MODE> st;
+          const v4i lo = *(const v4i*)(sp + wpo[2 * cc]);
+          const v4i hi = *(const v4i*)(sp + wpo[2 * cc + 1]);
+          if constexpr (MODE == M_FP8 || MODE == M_MXFP8) {
+            st.w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          } else {
+            st.lo = lo;
+            st.hi = hi;
+          }
+          if constexpr (MODE == M_MXFP8) {
+            st.s0 = *(const uint32_t*)(sp + spo + 4 * cc);
+          } else if constexpr (MODE == M_MXFP4) {
+            typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+            const v2u t2 = *(const v2u*)(sp + spo + 8 * cc);
+            st.s0 = t2.x;
+            st.s1 = t2.y;
+          }
+          compute_chunk_reg<MODE, NCT, NMW>(acc, st, 2 * ks + cc, g, xr);
+        }
+        // the slot's ds_reads have completed before the DMA may overwrite it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (iq < nst) issue_next((uint8_t*)sp);
+        ++q;
+        if (++slot == S) slot = 0;
+      }
+      AccV* hp = hand + ((s & 1) * NW + wave) * NCT * 64 + lane;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) hp[ct * 64] = acc.v[ct];
+    }
+    // hand-off written (lgkmcnt) before any wave reads it in the next step; the wave's
+    // weight DMA stays in flight across the barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
+}
+
 // The token of each batch row of a fused lm_head + sampling launch: one wave per row
 // reduces the row's per-wave keys.
 __global__ void __launch_bounds__(256) lmhead_sample_finish_kernel(const unsigned long long* skeys, int nslot,
@@ -1233,6 +1517,25 @@ static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, h
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 3, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
   else
     hipLaunchKernelGGL((lmhead_lds_kernel<MODE, NCT, 2, SMP>), dim3(grid), dim3(256), lds_bytes, st, a);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? VQK_OK : (int)e;
+}
+
+// Wide-batch form: the K slice of a wave is SPW 256-byte stages of every weight row, and the
+// waves of a workgroup cover the row (NW * SPW * 256 bytes).  Returns 0 when the row length
+// has no such split.
+template <int MODE>
+struct WideShape {
+  static constexpr int SPW = (MODE == M_MXFP4) ? 2 : 4;
+  static constexpr int NW = 3;
+  static bool fits(int KB) { return MODE != M_W8A16 && KB == NW * SPW * 256; }
+};
+
+template <int MODE, int NCT>
+static int launch_wide(const LmArgs& a, size_t lds_bytes, int grid, hipStream_t st) {
+  typedef WideShape<MODE> W;
+  hipLaunchKernelGGL((lmhead_wide_kernel<MODE, NCT, W::NW, W::SPW, LM_WIDE_STAGES>), dim3(grid), dim3(64 * (W::NW + 1)),
+                     lds_bytes, st, a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? VQK_OK : (int)e;
 }
@@ -1356,6 +1659,26 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     const size_t lds = xl.bytes(Bg);
     a.lds_x_bytes = (int)lds;
     const int ntiles = (int)((M + 15) / 16);
+    if constexpr (MODE != M_W8A16) {
+      typedef WideShape<MODE> W;
+      const int64_t left = B - b0;
+      if (lds_path && !smp && W::fits(KB) && left >= LM_WIDE_MIN_B && left <= 64) {
+        const int Bw = (int)left;
+        a.Bg = Bw;
+        a.glast_Bg = Bw;
+        const int nct_w = (Bw + 15) / 16;
+        const size_t ring_w = (size_t)W::NW * LM_WIDE_STAGES * G::SLOT;
+        const size_t hand_w = (size_t)2 * W::NW * nct_w * 64 * 16;
+        const size_t pro_w = xl.bytes(Bw < 32 ? Bw : 32);
+        const size_t lds_w = (ring_w + hand_w > pro_w) ? ring_w + hand_w : pro_w;
+        const int grid_w = ntiles < ncu ? ntiles : ncu;
+        const int rcw = (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
+                                     : launch_wide<MODE, 4>(a, lds_w, grid_w, st);
+        if (rcw) return rcw;
+        adv = Bw;
+        continue;
+      }
+    }
     if (lds_path && lds + ring2 <= lds_cap) {
       // The deepest ring (4, 3 or 2 stages per wave) that fits next to the activations.
       // W8A16 prefers two workgroups per CU (two waves per SIMD) with a shallower ring when
