@@ -63,8 +63,11 @@ constexpr int LM_W_POLICY = 2;
 //   in L2 (non-temporal pieces re-fetched it: 5.5% extra HBM reads, 3 us at MXFP4 batch 1).
 constexpr int LM_S_POLICY = 0;
 // - wide-batch kernel: weight ring stages per wave, and the smallest batch it serves;
-constexpr int LM_WIDE_STAGES = 8;
-constexpr int LM_WIDE_MIN_B = 33;
+constexpr int LM_WIDE_STAGES = 4;
+// - wide-batch kernel: tiles of logits its writer wave holds in registers beyond those
+//   that wait in LDS;
+constexpr int LM_WIDE_HOLD_REGS = 24;
+constexpr int LM_WIDE_MIN_B = 17;
 
 }  // namespace vqk
 
@@ -138,6 +141,7 @@ struct LmArgs {
   int ngrp;
   int64_t gs_x, gs_xq, gs_xsq, gs_out, gs_acc;
   int glast_Bg;
+  int wide_cap;         // wide-batch kernel: tiles whose logits wait in LDS for the end
   // fused Gumbel-argmax epilogue (the sampling form only)
   const float* stemp;   // [Bg] temperatures or null (greedy)
   const void* sseeds;   // [Bg] int32 or int64 seeds
@@ -1247,6 +1251,33 @@ __device__ __forceinline__ void load_xregs(XRegs<MODE, NCT, NMW>& xr, const LmAr
   }
 }
 
+// Pre-quantized activations (a.xq, and a.xsq for MX): the wave's fragments straight from
+// global memory into registers (row b's fragment (mi, g) is bytes frag_k(mi, g, 0..) of
+// the row, in runs of 16; an MX fragment's scale is the E8M0 byte of group 4mi + g), every
+// load issued before any is used, so the prologue costs one memory latency.
+template <int MODE, int NCT, int NMW>
+__device__ __forceinline__ void load_xregs_global(XRegs<MODE, NCT, NMW>& xr, const LmArgs& a, int mi0, int g, int j) {
+  typedef ModeTraits<MODE> T;
+  const int K = a.K;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int b = min(ct * 16 + j, a.Bg - 1);
+    const uint8_t* row = a.xq + (int64_t)b * K;
+#pragma unroll
+    for (int ml = 0; ml < NMW; ++ml) {
+      const int mi = mi0 + ml;
+      if constexpr (T::FB == 32) {
+        const v4i b0 = *(const v4i*)(row + frag_k<MODE>(mi, g, 0));
+        const v4i b1 = *(const v4i*)(row + frag_k<MODE>(mi, g, 16));
+        xr.f[ct][ml] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+        xr.f[ct][ml] = __builtin_bit_cast(typename FragT<MODE>::type, *(const v4i*)(row + frag_k<MODE>(mi, g, 0)));
+      }
+      if constexpr (T::MX) xr.sb[ct][ml] = a.xsq[(int64_t)b * (K >> 5) + 4 * mi + g];
+    }
+  }
+}
+
 // compute_chunk() with the B fragments of the wave's local chunk cl taken from registers.
 template <int MODE, int NCT, int NMW>
 __device__ __forceinline__ void compute_chunk_reg(Acc<MODE, NCT>& acc, const Slot<MODE>& s, int cl, int g,
@@ -1339,18 +1370,33 @@ lmhead_wide_kernel(LmArgs a) {
     if (wave < NW) load_xregs<MODE, NCT, NMW>(xr, ah, smem, lxs, h, wave * NMW, g, r);
     __syncthreads();
   };
-  stage_half(IntTag<0>{});
-  if constexpr (NCT > 2) stage_half(IntTag<1>{});
+  // (pre-quantized activations in 16-byte aligned rows skip the staging)
+  const bool direct = a.xq != nullptr && a.xvec && (!T::MX || a.xsq != nullptr);
+  if (direct) {
+    if (MODE == M_W8A8) xs_w8a8 = a.xs_dev ? *a.xs_dev : a.xs_val;
+    if (wave < NW) load_xregs_global<MODE, NCT, NMW>(xr, a, wave * NMW, g, r);
+  } else {
+    stage_half(IntTag<0>{});
+    if constexpr (NCT > 2) stage_half(IntTag<1>{});
+  }
 
-  // LDS: the compute waves' rings, then the accumulator hand-off [2][NW][NCT][64 lanes]:
-  // slot w of a step holds compute wave w's accumulators (slot NW - 1: the finished tile).
+  // LDS: the compute waves' rings, then the accumulator hand-off [2][NW][NCT][64 lanes]
+  // (slot w of a step holds compute wave w's accumulators; slot NW - 1 the finished tile),
+  // then the held logits [NCT * 16 batch rows][HROW bytes]: tile i's 16 rows at 32i.
   AccV* hand = (AccV*)(smem + NW * S * G::SLOT);
+  uint8_t* hold = smem + NW * S * G::SLOT + 2 * NW * NCT * 64 * (int)sizeof(AccV);
+  const int cap = a.wide_cap;
+  const int hrow = cap * 32 + 16;  // +16: the 16 batch rows of one ds_write hit distinct banks
   const int nsteps = my_tiles + NW;
   if (wave == NW) {
-    // The writer: dequantizes and stores each finished tile one step after the last
-    // compute wave handed it over.  It issues no weight loads, so no stage wait ever waits
-    // for a store (stores and loads retire in order through one counter).
+    // The writer dequantizes each finished tile one step after the last compute wave
+    // handed it over, and keeps its logits until the weight stream ends: the first cap
+    // tiles in LDS, the next LM_WIDE_HOLD_REGS in its registers (each new tile shifts the
+    // held ones down a slot), any further tile stored at once.  Logits written while the
+    // weight streams cost ~20 % of the stream at batch 64, whatever their layout.
     uint32_t sdw[16];
+    uint2 ob[LM_WIDE_HOLD_REGS][NCT];
+    int nreg = 0;
     for (int s = 0; s < nsteps; ++s) {
       const int i = s - NW;
       if (i >= 0) {
@@ -1375,13 +1421,28 @@ lmhead_wide_kernel(LmArgs a) {
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) nv[ct] = make_uint2(0u, 0u);
         epilogue<MODE, NCT>(acc, a, ctile * 16, lane, xs_w8a8, tsc, nv, nullptr);
-        store_tile<NCT>(a, ctile * 16, lane, nv);
+        if (i < cap) {
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) *(uint2*)(hold + (ct * 16 + r) * hrow + 32 * i + 8 * g) = nv[ct];
+        } else if (nreg < LM_WIDE_HOLD_REGS) {
+#pragma unroll
+          for (int k = 0; k + 1 < LM_WIDE_HOLD_REGS; ++k)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) ob[k][ct] = ob[k + 1][ct];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) ob[LM_WIDE_HOLD_REGS - 1][ct] = nv[ct];
+          ++nreg;
+        } else {
+          store_tile<NCT>(a, ctile * 16, lane, nv);
+        }
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    return;
-  }
-
+    // the register-held tiles: slot k holds tile cap + k - (LM_WIDE_HOLD_REGS - nreg)
+#pragma unroll
+    for (int k = 0; k < LM_WIDE_HOLD_REGS; ++k)
+      if (k >= LM_WIDE_HOLD_REGS - nreg) store_tile<NCT>(a, (t0 + cap + k - (LM_WIDE_HOLD_REGS - nreg)) * 16, lane, ob[k]);
+  } else {
   uint8_t* ring = smem + wave * (S * G::SLOT);
   IssueOffsets<MODE> io;
   const int nst = my_tiles * SPW;
@@ -1459,7 +1520,27 @@ lmhead_wide_kernel(LmArgs a) {
     // weight DMA stays in flight across the barrier
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
-  wait_vmcnt<0>();  // no DMA into LDS may still be in flight when the wave retires
+  wait_vmcnt<0>();  // no DMA into LDS may still be in flight past this point
+  }
+  // The weight stream is done: every wave stores the LDS-held logits, batch row by batch
+  // row, in 16-byte pieces of consecutive rows (full 128-byte lines).
+  __syncthreads();
+  const int nh = min(my_tiles, cap);
+  const bool vec16 = ((uintptr_t)a.out & 15) == 0 && (a.ldo & 7) == 0;
+  for (int u = threadIdx.x; u < a.Bg * 2 * nh; u += 64 * (NW + 1)) {
+    const int b = u / (2 * nh), p = u - b * (2 * nh);
+    const int r0 = t0 * 16 + 8 * p;
+    const v4i v = *(const v4i*)(hold + b * hrow + 16 * p);
+    uint16_t* op = a.out + (int64_t)b * a.ldo + r0;
+    if (vec16 && r0 + 8 <= a.M) {
+      *(v4i*)op = v;
+    } else {
+      const uint32_t w4[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (r0 + e < a.M) op[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+    }
+  }
 }
 
 // The token of each batch row of a fused lm_head + sampling launch: one wave per row
@@ -1666,14 +1747,22 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         const int Bw = (int)left;
         a.Bg = Bw;
         a.glast_Bg = Bw;
-        const int nct_w = (Bw + 15) / 16;
+        const int nct_w = Bw <= 32 ? 2 : (Bw + 15) / 16;  // the kernel's column tiles
         const size_t ring_w = (size_t)W::NW * LM_WIDE_STAGES * G::SLOT;
         const size_t hand_w = (size_t)2 * W::NW * nct_w * 64 * 16;
         const size_t pro_w = xl.bytes(Bw < 32 ? Bw : 32);
-        const size_t lds_w = (ring_w + hand_w > pro_w) ? ring_w + hand_w : pro_w;
         const int grid_w = ntiles < ncu ? ntiles : ncu;
-        const int rcw = (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
-                                     : launch_wide<MODE, 4>(a, lds_w, grid_w, st);
+        // the most tiles a workgroup streams, and how many of them LDS can hold
+        const int tmax = (ntiles + grid_w - 1) / grid_w;
+        const size_t avail = (size_t)159 * 1024 - ring_w - hand_w;
+        int cap = (int)((avail / ((size_t)nct_w * 16) - 16) / 32);
+        if (cap > tmax) cap = tmax;
+        a.wide_cap = cap;
+        const size_t held_w = (size_t)nct_w * 16 * ((size_t)cap * 32 + 16);
+        const size_t lds_w = (ring_w + hand_w + held_w > pro_w) ? ring_w + hand_w + held_w : pro_w;
+        const int rcw = (nct_w <= 2)   ? launch_wide<MODE, 2>(a, lds_w, grid_w, st)
+                        : (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
+                                       : launch_wide<MODE, 4>(a, lds_w, grid_w, st);
         if (rcw) return rcw;
         adv = Bw;
         continue;
