@@ -1333,6 +1333,11 @@ lmhead_wide_kernel(LmArgs a) {
   constexpr int NMW = 2 * SPW * T::MPC;  // MFMAs per column tile of a wave's slice of a row
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float red[17];
+  __shared__ int nreg_lds;
+  // row stride of the writer's register tiles parked in the ring's LDS after the stream
+  constexpr int HROW2 = LM_WIDE_HOLD_REGS * 32 + 16;
+  static_assert(NCT * 16 * HROW2 <= NW * S * G::SLOT + 2 * NW * NCT * 64 * (int)sizeof(typename AccT<MODE>::type),
+                "the parked tiles must fit the ring and hand-off space");
   const int K = a.K;
   const int KB = (MODE == M_MXFP4) ? (K >> 1) : K;
   const int lane = threadIdx.x & 63;
@@ -1438,10 +1443,18 @@ lmhead_wide_kernel(LmArgs a) {
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    // the register-held tiles: slot k holds tile cap + k - (LM_WIDE_HOLD_REGS - nreg)
+    // the register-held tiles (slot k: tile cap + k - (LM_WIDE_HOLD_REGS - nreg)) go to the
+    // ring's LDS once every compute wave is past its stream, in the held layout
+    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < LM_WIDE_HOLD_REGS; ++k)
-      if (k >= LM_WIDE_HOLD_REGS - nreg) store_tile<NCT>(a, (t0 + cap + k - (LM_WIDE_HOLD_REGS - nreg)) * 16, lane, ob[k]);
+    for (int k = 0; k < LM_WIDE_HOLD_REGS; ++k) {
+      const int i2 = k - (LM_WIDE_HOLD_REGS - nreg);
+      if (i2 >= 0) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) *(uint2*)(smem + (ct * 16 + r) * HROW2 + 32 * i2 + 8 * g) = ob[k][ct];
+      }
+    }
+    if (lane == 0) nreg_lds = nreg;
   } else {
   uint8_t* ring = smem + wave * (S * G::SLOT);
   IssueOffsets<MODE> io;
@@ -1521,26 +1534,32 @@ lmhead_wide_kernel(LmArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   wait_vmcnt<0>();  // no DMA into LDS may still be in flight past this point
+  __syncthreads();   // (the writer's first barrier after the stream)
   }
-  // The weight stream is done: every wave stores the LDS-held logits, batch row by batch
-  // row, in 16-byte pieces of consecutive rows (full 128-byte lines).
+  // The weight stream is done: every wave stores the held logits, batch row by batch row,
+  // in 16-byte pieces of consecutive rows (full 128-byte lines): first the cap tiles held
+  // in LDS from the start, then the writer's register tiles parked in the ring's LDS.
   __syncthreads();
-  const int nh = min(my_tiles, cap);
+  const int nh = min(my_tiles, cap), n2 = nreg_lds;
   const bool vec16 = ((uintptr_t)a.out & 15) == 0 && (a.ldo & 7) == 0;
-  for (int u = threadIdx.x; u < a.Bg * 2 * nh; u += 64 * (NW + 1)) {
-    const int b = u / (2 * nh), p = u - b * (2 * nh);
-    const int r0 = t0 * 16 + 8 * p;
-    const v4i v = *(const v4i*)(hold + b * hrow + 16 * p);
-    uint16_t* op = a.out + (int64_t)b * a.ldo + r0;
-    if (vec16 && r0 + 8 <= a.M) {
-      *(v4i*)op = v;
-    } else {
-      const uint32_t w4[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+  auto flush = [&](const uint8_t* src, int rowb, int nt, int tfirst) {
+    for (int u = threadIdx.x; u < a.Bg * 2 * nt; u += 64 * (NW + 1)) {
+      const int b = u / (2 * nt), p = u - b * (2 * nt);
+      const int r0 = tfirst * 16 + 8 * p;
+      const v4i v = *(const v4i*)(src + b * rowb + 16 * p);
+      uint16_t* op = a.out + (int64_t)b * a.ldo + r0;
+      if (vec16 && r0 + 8 <= a.M) {
+        *(v4i*)op = v;
+      } else {
+        const uint32_t w4[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (r0 + e < a.M) op[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+        for (int e = 0; e < 8; ++e)
+          if (r0 + e < a.M) op[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+      }
     }
-  }
+  };
+  flush(hold, hrow, nh, t0);
+  if (n2 > 0) flush(smem, HROW2, n2, t0 + cap);
 }
 
 // The token of each batch row of a fused lm_head + sampling launch: one wave per row
