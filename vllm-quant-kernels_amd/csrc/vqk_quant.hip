@@ -173,6 +173,23 @@ __global__ void act_cast_e4m3_kernel(const void* x, int dt, int64_t ldx, int64_t
   xq[i] = f32_to_e4m3(load_as_f32(x, dt, b * ldx + k));
 }
 
+// The same cast, 8 consecutive elements per thread: one 16-byte load (fp16/bf16; two for
+// fp32), the hardware conversion with torch's NaN and overflow semantics (e4m3x4_torch,
+// equal to f32_to_e4m3 on every float32) and one 8-byte store, with 32-bit indices.  At
+// activation sizes the launch is a few latencies long, so the per-element form's 64-bit
+// division and byte stores were most of it.
+template <int DT>
+__global__ void __launch_bounds__(256) act_cast_e4m3_vec_kernel(const void* x, int64_t ldx, int per_row, int total,
+                                                                uint8_t* xq) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= total) return;
+  const int b = c / per_row, k8 = c - b * per_row;
+  float v[8];
+  load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v);
+  *(uint2*)(xq + (int64_t)b * per_row * 8 + 8 * k8) =
+      make_uint2(e4m3x4_torch(v[0], v[1], v[2], v[3]), e4m3x4_torch(v[4], v[5], v[6], v[7]));
+}
+
 static int dt_ok(int dt) { return dt == VQK_F32 || dt == VQK_F16 || dt == VQK_BF16; }
 
 static int finish() {
@@ -272,6 +289,18 @@ extern "C" int vqk_act_cast_e4m3(const void* x, int x_dtype, int64_t ldx, int64_
   if (!x || !xq || !dt_ok(x_dtype) || B < 0 || K < 1 || ldx < K) return VQK_EINVAL;
   if (B == 0) return VQK_OK;
   const int64_t n = B * K;
+  const int es = (x_dtype == VQK_F32) ? 4 : 2;
+  const bool vec = K % 8 == 0 && ((uintptr_t)x & 15) == 0 && (ldx * es) % 16 == 0 && ((uintptr_t)xq & 7) == 0 &&
+                   n / 8 < (int64_t)INT32_MAX - 256;
+  if (vec) {
+    const int per_row = (int)(K / 8), total = (int)(n / 8);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    const hipStream_t st = (hipStream_t)stream;
+    if (x_dtype == VQK_F32) hipLaunchKernelGGL(act_cast_e4m3_vec_kernel<VQK_F32>, grid, dim3(256), 0, st, x, ldx, per_row, total, xq);
+    else if (x_dtype == VQK_F16) hipLaunchKernelGGL(act_cast_e4m3_vec_kernel<VQK_F16>, grid, dim3(256), 0, st, x, ldx, per_row, total, xq);
+    else hipLaunchKernelGGL(act_cast_e4m3_vec_kernel<VQK_BF16>, grid, dim3(256), 0, st, x, ldx, per_row, total, xq);
+    return finish();
+  }
   hipLaunchKernelGGL(act_cast_e4m3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      x, x_dtype, ldx, B, K, xq);
   return finish();
