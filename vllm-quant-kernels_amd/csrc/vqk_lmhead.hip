@@ -26,6 +26,11 @@
 //    (a store burst then, instead of stores queued behind the weight loads).
 //  * Batches beyond one group's LDS budget run up to four XCD-grouped batch groups in one
 //    launch, so the later readers of each weight line find it in L2 or the last-level cache.
+//  * Batch rows 17-64 at K = 3072 (9-32 per launch for W8A16), lmhead_wide_kernel: the
+//    waves of a workgroup split K instead of rows (three compute waves, six for W8A16),
+//    keep their slice of every row's activation fragments in VGPRs, pass the partial
+//    accumulators from wave to wave through LDS, and a writer wave holds the logits until
+//    the weight stream ends.
 //  * Fallback, lmhead_kernel: when K or the scale alignment rules out 256-byte stages, a
 //    512-thread kernel keeps a D-deep ring of 128-byte chunks per lane in registers; same
 //    prologue, MFMA and epilogue code.
@@ -68,6 +73,9 @@ constexpr int LM_WIDE_STAGES = 4;
 //   that wait in LDS;
 constexpr int LM_WIDE_HOLD_REGS = 24;
 constexpr int LM_WIDE_MIN_B = 17;
+// (W8A16 at 248320 x 3072, us per call, row-tiled / wide: B=8 116.2-117.6 / 121.4-121.7,
+// B=10 124.5-125.2 / 122.1-122.5, B=16 123.5-126.1 / 124.0-124.2, B=17 205-207 / 125-127)
+constexpr int LM_WIDE_MIN_B_W8A16 = 9;
 
 }  // namespace vqk
 
@@ -1259,6 +1267,17 @@ template <int MODE, int NCT, int NMW>
 __device__ __forceinline__ void load_xregs_global(XRegs<MODE, NCT, NMW>& xr, const LmArgs& a, int mi0, int g, int j) {
   typedef ModeTraits<MODE> T;
   const int K = a.K;
+  if constexpr (MODE == M_W8A16) {
+    // fp16 activations as they are: fragment (mi, g) is the 8 elements from frag_k(mi, g, 0)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const uint16_t* row = (const uint16_t*)a.x + (int64_t)min(ct * 16 + j, a.Bg - 1) * a.ldx;
+#pragma unroll
+      for (int ml = 0; ml < NMW; ++ml)
+        xr.f[ct][ml] = __builtin_bit_cast(v8h, *(const v4i*)(row + frag_k<MODE>(mi0 + ml, g, 0)));
+    }
+    return;
+  }
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) {
     const int b = min(ct * 16 + j, a.Bg - 1);
@@ -1325,7 +1344,7 @@ __device__ __forceinline__ void compute_chunk_reg(Acc<MODE, NCT>& acc, const Slo
 }
 
 template <int MODE, int NCT, int NW, int SPW, int S>
-__global__ void __launch_bounds__(64 * (NW + 1)) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(64 * (NW + 1)) __attribute__((amdgpu_waves_per_eu(1, (NW + 4) / 4)))
 lmhead_wide_kernel(LmArgs a) {
   typedef ModeTraits<MODE> T;
   typedef StageGeom<MODE> G;
@@ -1375,9 +1394,12 @@ lmhead_wide_kernel(LmArgs a) {
     if (wave < NW) load_xregs<MODE, NCT, NMW>(xr, ah, smem, lxs, h, wave * NMW, g, r);
     __syncthreads();
   };
-  // (pre-quantized activations in 16-byte aligned rows skip the staging)
+  // (pre-quantized activations in 16-byte aligned rows skip the staging, and so do W8A16's
+  // fp16 activations, for which the host launches this form only with aligned rows)
   const bool direct = a.xq != nullptr && a.xvec && (!T::MX || a.xsq != nullptr);
-  if (direct) {
+  if constexpr (MODE == M_W8A16) {
+    if (wave < NW) load_xregs_global<MODE, NCT, NMW>(xr, a, wave * NMW, g, r);
+  } else if (direct) {
     if (MODE == M_W8A8) xs_w8a8 = a.xs_dev ? *a.xs_dev : a.xs_val;
     if (wave < NW) load_xregs_global<MODE, NCT, NMW>(xr, a, wave * NMW, g, r);
   } else {
@@ -1624,11 +1646,16 @@ static int launch_lds(const LmArgs& a, int stages, size_t lds_bytes, int grid, h
 // Wide-batch form: the K slice of a wave is SPW 256-byte stages of every weight row, and the
 // waves of a workgroup cover the row (NW * SPW * 256 bytes).  Returns 0 when the row length
 // has no such split.
+// W8A16 keeps fp16 fragments (four per 128 weight bytes), so its K splits six ways (two
+// waves per SIMD) and a launch covers at most 32 batch rows (2 column tiles: 128 VGPRs of
+// fragments per wave).
 template <int MODE>
 struct WideShape {
-  static constexpr int SPW = (MODE == M_MXFP4) ? 2 : 4;
-  static constexpr int NW = 3;
-  static bool fits(int KB) { return MODE != M_W8A16 && KB == NW * SPW * 256; }
+  static constexpr int SPW = (MODE == M_MXFP4 || MODE == M_W8A16) ? 2 : 4;
+  static constexpr int NW = (MODE == M_W8A16) ? 6 : 3;
+  static constexpr int MAXB = (MODE == M_W8A16) ? 32 : 64;
+  static constexpr int MINB = (MODE == M_W8A16) ? LM_WIDE_MIN_B_W8A16 : LM_WIDE_MIN_B;
+  static bool fits(int KB) { return KB == NW * SPW * 256; }
 };
 
 template <int MODE, int NCT>
@@ -1759,17 +1786,21 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     const size_t lds = xl.bytes(Bg);
     a.lds_x_bytes = (int)lds;
     const int ntiles = (int)((M + 15) / 16);
-    if constexpr (MODE != M_W8A16) {
+    {
       typedef WideShape<MODE> W;
       const int64_t left = B - b0;
-      if (lds_path && !smp && W::fits(KB) && left >= LM_WIDE_MIN_B && left <= 64) {
-        const int Bw = (int)left;
+      // W8A16 reads its fp16 activations straight into registers (aligned rows only) and
+      // splits more than 32 rows into balanced launches of at most 32
+      const bool xok = MODE != M_W8A16 || (xdt == VQK_F16 && a.xvec);
+      const int64_t nwl = (MODE == M_W8A16) ? (left + W::MAXB - 1) / W::MAXB : 1;
+      if (lds_path && !smp && xok && W::fits(KB) && left >= W::MINB && (MODE == M_W8A16 || left <= W::MAXB)) {
+        const int Bw = (int)((left + nwl - 1) / nwl);
         a.Bg = Bw;
         a.glast_Bg = Bw;
         const int nct_w = Bw <= 32 ? 2 : (Bw + 15) / 16;  // the kernel's column tiles
         const size_t ring_w = (size_t)W::NW * LM_WIDE_STAGES * G::SLOT;
         const size_t hand_w = (size_t)2 * W::NW * nct_w * 64 * 16;
-        const size_t pro_w = xl.bytes(Bw < 32 ? Bw : 32);
+        const size_t pro_w = (MODE == M_W8A16) ? 0 : xl.bytes(Bw < 32 ? Bw : 32);
         const int grid_w = ntiles < ncu ? ntiles : ncu;
         // the most tiles a workgroup streams, and how many of them LDS can hold
         const int tmax = (ntiles + grid_w - 1) / grid_w;
@@ -1779,9 +1810,13 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         a.wide_cap = cap;
         const size_t held_w = (size_t)nct_w * 16 * ((size_t)cap * 32 + 16);
         const size_t lds_w = (ring_w + hand_w + held_w > pro_w) ? ring_w + hand_w + held_w : pro_w;
-        const int rcw = (nct_w <= 2)   ? launch_wide<MODE, 2>(a, lds_w, grid_w, st)
-                        : (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
-                                       : launch_wide<MODE, 4>(a, lds_w, grid_w, st);
+        int rcw;
+        if constexpr (W::MAXB <= 32)
+          rcw = launch_wide<MODE, 2>(a, lds_w, grid_w, st);
+        else
+          rcw = (nct_w <= 2)   ? launch_wide<MODE, 2>(a, lds_w, grid_w, st)
+                : (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
+                               : launch_wide<MODE, 4>(a, lds_w, grid_w, st);
         if (rcw) return rcw;
         adv = Bw;
         continue;
