@@ -122,15 +122,36 @@ __global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int
   // 32-bit indices (B * K / 8 < 2^31 on the vector path): a 64-bit division per step
   // would cost more than the loads
   const int per_row = (int)(K / 8), total = (int)B * per_row;
+  const bool contig = ldx == K;
   float m = 0.f;
   if (vec) {
-#pragma unroll 4
-    for (int c = threadIdx.x; c < total; c += blockDim.x) {
-      const int b = c / per_row, k8 = c - b * per_row;
-      float v[8];
-      load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v);
+    // The whole tensor in rounds of AQ_LOADS 8-element chunks per thread, every load of a
+    // round issued before any is used (each round costs one L2 latency).  Chunks past the
+    // end re-read the thread's first chunk of the round, which changes no maximum.  Rows
+    // stored back to back (ldx == K) address chunk c at 8c: the division by the row length
+    // (a ~40-instruction sequence per chunk) was most of the launch.
+    constexpr int AQ_LOADS = (DT == VQK_F32) ? 8 : 16;
+    for (int c0 = threadIdx.x; c0 < total; c0 += AQ_LOADS * (int)blockDim.x) {
+      float v[AQ_LOADS][8];
+      if (contig) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+        for (int u = 0; u < AQ_LOADS; ++u) {
+          const int c = c0 + u * (int)blockDim.x;
+          load_run<DT, 8>(x, (int64_t)8 * (c < total ? c : c0), true, v[u]);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < AQ_LOADS; ++u) {
+          int c = c0 + u * (int)blockDim.x;
+          c = c < total ? c : c0;
+          const int b = c / per_row, k8 = c - b * per_row;
+          load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < AQ_LOADS; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[u][e]));
     }
   } else {
     for (int64_t b = 0; b < B; ++b)
@@ -145,16 +166,20 @@ __global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int
     const int c0 = blockIdx.x * share, c1 = min(total, c0 + share);
 #pragma unroll 2
     for (int c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
-      const int b = c / per_row, k8 = c - b * per_row;
+      int64_t off = (int64_t)8 * c;
+      if (!contig) {
+        const int b = c / per_row, k8 = c - b * per_row;
+        off = (int64_t)b * ldx + 8 * k8;
+      }
       float v[8];
-      load_run<DT, 8>(x, (int64_t)b * ldx + 8 * k8, true, v);
+      load_run<DT, 8>(x, off, true, v);
       uint32_t w[2] = {0u, 0u};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float q = fminf(fmaxf(rint_div_i8(v[e], s, r), -127.f), 127.f);
         w[e >> 2] |= ((uint32_t)(int)q & 0xFFu) << (8 * (e & 3));
       }
-      *(uint2*)(xq + (int64_t)b * K + 8 * k8) = make_uint2(w[0], w[1]);
+      *(uint2*)(xq + (int64_t)8 * c) = make_uint2(w[0], w[1]);  // xq rows are K apart
     }
   } else if (blockIdx.x == 0) {
     for (int64_t b = 0; b < B; ++b)
