@@ -130,7 +130,7 @@ __global__ void __launch_bounds__(1024) act_quant_int8_kernel(const void* x, int
     // end re-read the thread's first chunk of the round, which changes no maximum.  Rows
     // stored back to back (ldx == K) address chunk c at 8c: the division by the row length
     // (a ~40-instruction sequence per chunk) was most of the launch.
-    constexpr int AQ_LOADS = (DT == VQK_F32) ? 8 : 16;
+    constexpr int AQ_LOADS = (DT == VQK_F16) ? 16 : 8;  // (bf16 at 16 spills)
     for (int c0 = threadIdx.x; c0 < total; c0 += AQ_LOADS * (int)blockDim.x) {
       float v[AQ_LOADS][8];
       if (contig) {
