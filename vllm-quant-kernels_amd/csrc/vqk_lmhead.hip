@@ -76,6 +76,10 @@ constexpr int LM_WIDE_MIN_B = 17;
 // (W8A16 at 248320 x 3072, us per call, row-tiled / wide: B=8 116.2-117.6 / 121.4-121.7,
 // B=10 124.5-125.2 / 122.1-122.5, B=16 123.5-126.1 / 124.0-124.2, B=17 205-207 / 125-127)
 constexpr int LM_WIDE_MIN_B_W8A16 = 9;
+// (batches above 64 rows, us per call, grouped row-tiled / balanced wide launches: FP8 80
+// 240 / 252, 96 257 / 256, 128 315 / 268, 256 625 / 527; MXFP8 96 278 / 261, 128 342 / 271;
+// W8A8 96 272 / 264, 128 335 / 278; MXFP4 80 176 / 166, 128 214 / 189)
+constexpr int LM_WIDE_SPLIT_MIN_B = 96;
 
 }  // namespace vqk
 
@@ -1655,6 +1659,7 @@ struct WideShape {
   static constexpr int NW = (MODE == M_W8A16) ? 6 : 3;
   static constexpr int MAXB = (MODE == M_W8A16) ? 32 : 64;
   static constexpr int MINB = (MODE == M_W8A16) ? LM_WIDE_MIN_B_W8A16 : LM_WIDE_MIN_B;
+  static constexpr int SPLIT_MIN_B = (MODE == M_W8A16 || MODE == M_MXFP4) ? MAXB + 1 : LM_WIDE_SPLIT_MIN_B;
   static bool fits(int KB) { return KB == NW * SPW * 256; }
 };
 
@@ -1789,11 +1794,13 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
     {
       typedef WideShape<MODE> W;
       const int64_t left = B - b0;
-      // W8A16 reads its fp16 activations straight into registers (aligned rows only) and
-      // splits more than 32 rows into balanced launches of at most 32
+      // W8A16 reads its fp16 activations straight into registers (aligned rows only).
+      // Batches above MAXB rows run as balanced launches of at most MAXB, each streaming the
+      // weight once (W8A16 and MXFP4 from MAXB + 1 rows, the 8-bit modes from 96).
       const bool xok = MODE != M_W8A16 || (xdt == VQK_F16 && a.xvec);
-      const int64_t nwl = (MODE == M_W8A16) ? (left + W::MAXB - 1) / W::MAXB : 1;
-      if (lds_path && !smp && xok && W::fits(KB) && left >= W::MINB && (MODE == M_W8A16 || left <= W::MAXB)) {
+      const int64_t nwl = (left + W::MAXB - 1) / W::MAXB;
+      const bool split_ok = left <= W::MAXB || left >= W::SPLIT_MIN_B;
+      if (lds_path && !smp && xok && W::fits(KB) && left >= W::MINB && split_ok) {
         const int Bw = (int)((left + nwl - 1) / nwl);
         a.Bg = Bw;
         a.glast_Bg = Bw;
