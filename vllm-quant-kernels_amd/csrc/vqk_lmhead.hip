@@ -73,8 +73,10 @@ constexpr int LM_WIDE_STAGES = 4;
 //   that wait in LDS;
 constexpr int LM_WIDE_HOLD_REGS = 24;
 constexpr int LM_WIDE_MIN_B = 17;
-// (W8A16 at 248320 x 3072, us per call, row-tiled / wide: B=8 116.2-117.6 / 121.4-121.7,
-// B=10 124.5-125.2 / 122.1-122.5, B=16 123.5-126.1 / 124.0-124.2, B=17 205-207 / 125-127)
+// (W8A16 at 248320 x 3072, us per call, row-tiled / wide: B=8 116.2-117.6 / 121.4-121.7
+// (two column tiles), B=9 ~125 / 120.7-120.9 and B=16 123.5-126.1 / 120.3-120.9 (one
+// tile), B=17 205-207 / 124-127; the 8-bit modes on one tile at 9-16 rows were within
+// noise of the row-tiled kernel: FP8 B=16 121.4 / 123.3, MXFP4 B=9 70.1 / 68.6)
 constexpr int LM_WIDE_MIN_B_W8A16 = 9;
 // (batches above 64 rows, us per call, grouped row-tiled / balanced wide launches: FP8 80
 // 240 / 252, 96 257 / 256, 128 315 / 268, 256 625 / 527; MXFP8 96 278 / 261, 128 342 / 271;
@@ -1804,7 +1806,9 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         const int Bw = (int)((left + nwl - 1) / nwl);
         a.Bg = Bw;
         a.glast_Bg = Bw;
-        const int nct_w = Bw <= 32 ? 2 : (Bw + 15) / 16;  // the kernel's column tiles
+        // the kernel's column tiles (the 8-bit modes start at 17 rows; W8A16 runs 9-16 rows
+        // on one tile)
+        const int nct_w = (MODE == M_W8A16 && Bw <= 16) ? 1 : (Bw <= 32 ? 2 : (Bw + 15) / 16);
         const size_t ring_w = (size_t)W::NW * LM_WIDE_STAGES * G::SLOT;
         const size_t hand_w = (size_t)2 * W::NW * nct_w * 64 * 16;
         const size_t pro_w = (MODE == M_W8A16) ? 0 : xl.bytes(Bw < 32 ? Bw : 32);
@@ -1819,7 +1823,7 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         const size_t lds_w = (ring_w + hand_w + held_w > pro_w) ? ring_w + hand_w + held_w : pro_w;
         int rcw;
         if constexpr (W::MAXB <= 32)
-          rcw = launch_wide<MODE, 2>(a, lds_w, grid_w, st);
+          rcw = (nct_w == 1) ? launch_wide<MODE, 1>(a, lds_w, grid_w, st) : launch_wide<MODE, 2>(a, lds_w, grid_w, st);
         else
           rcw = (nct_w <= 2)   ? launch_wide<MODE, 2>(a, lds_w, grid_w, st)
                 : (nct_w == 3) ? launch_wide<MODE, 3>(a, lds_w, grid_w, st)
