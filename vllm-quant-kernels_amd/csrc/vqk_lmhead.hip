@@ -1845,6 +1845,11 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         return (size_t)per_cu * (lds + (size_t)4 * n * G::SLOT + 512) <= (per_cu == 1 ? lds_cap : 160 * 1024);
       };
       int per_cu_l = 1, stages = 0;
+      // W8A16 at batch 1: four workgroups per CU on 2-stage rings where they fit (16 waves
+      // hide the conversion and MFMA latency best while the shader clock settles: headline
+      // window 118.9-119.6 vs 119.0-120.1 us, first 100 calls 117.2-117.4 vs 117.9-118.7,
+      // steady state 112.5-112.8 vs 113.8-114.2 with two per CU; three per CU: 127)
+      if (MODE == M_W8A16 && !smp && fits(2, 4)) stages = 2, per_cu_l = 4;
       if (MODE == M_W8A16 && !smp)
         for (int n = 4; n >= 2 && !stages; --n)
           if (fits(n, 2)) stages = n, per_cu_l = 2;
