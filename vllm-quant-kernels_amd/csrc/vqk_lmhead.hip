@@ -1849,8 +1849,11 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
       // hide the conversion and MFMA latency best while the shader clock settles: headline
       // window 118.9-119.6 vs 119.0-120.1 us, first 100 calls 117.2-117.4 vs 117.9-118.7,
       // steady state 112.5-112.8 vs 113.8-114.2 with two per CU; three per CU: 127)
+      // FP8 and MXFP4 at 1-4 rows: two per CU (FP8 B=1 111.6-111.9 vs 113.1-114.5 us, MXFP4
+      // B=4 63.2 vs 63.8-64.0; at 8 rows 0.5 us slower); MXFP8 keeps one (B=4 118.1-118.4 vs
+      // 115.8-115.9), W8A8 measured the same either way.
       if (MODE == M_W8A16 && !smp && fits(2, 4)) stages = 2, per_cu_l = 4;
-      if (MODE == M_W8A16 && !smp)
+      if ((MODE == M_W8A16 || ((MODE == M_FP8 || MODE == M_MXFP4) && Bg <= 4)) && !smp)
         for (int n = 4; n >= 2 && !stages; --n)
           if (fits(n, 2)) stages = n, per_cu_l = 2;
       if (!stages) stages = fits(4, 1) ? 4 : fits(3, 1) ? 3 : 2;
