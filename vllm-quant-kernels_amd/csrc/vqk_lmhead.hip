@@ -1577,7 +1577,14 @@ lmhead_wide_kernel(LmArgs a) {
       const v4i v = *(const v4i*)(src + b * rowb + 16 * p);
       uint16_t* op = a.out + (int64_t)b * a.ldo + r0;
       if (vec16 && r0 + 8 <= a.M) {
-        *(v4i*)op = v;
+        // non-temporal: the logits are not read back here, so they bypass the caches
+        // (µs per call, cached / non-temporal: FP8 B=64 136.5-137.7 / 135.1-136.0, W8A8
+        // B=64 142.3-143.3 / 140.3-141.3, W8A16 B=32 128.4-129.1 / 126.5-127.8, MXFP4 B=32
+        // 73.8-74.1 / 72.8-73.8; MXFP8 B=64 138.1-138.4 / 138.9-139.8 keeps cached stores)
+        if constexpr (MODE == M_MXFP8)
+          *(v4i*)op = v;
+        else
+          __builtin_nontemporal_store(v, (v4i*)op);
       } else {
         const uint32_t w4[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
