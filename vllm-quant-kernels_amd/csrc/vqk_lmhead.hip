@@ -1349,6 +1349,15 @@ __device__ __forceinline__ void compute_chunk_reg(Acc<MODE, NCT>& acc, const Slo
   }
 }
 
+// How the K-split form deals its 16-row tiles to workgroups (µs per call at 248320 x 3072,
+// contiguous ranges / groups of 4: FP8 B=64 135.4-135.6 / 134.5-135.3, MXFP8 B=64
+// 138.4-138.5 / 136.9-137.0, W8A8 B=64 142.1-142.6 / 138.9-139.7, W8A16 B=32 within
+// noise; MXFP4 B=32 72.9-73.0 / 75.3-76.2, and slower still with groups of 8, 16 or 32).
+template <int MODE>
+struct WideTileGroup {
+  static constexpr int TG = (MODE == M_MXFP4) ? 0 : 4;
+};
+
 template <int MODE, int NCT, int NW, int SPW, int S>
 __global__ void __launch_bounds__(64 * (NW + 1)) __attribute__((amdgpu_waves_per_eu(1, (NW + 4) / 4)))
 lmhead_wide_kernel(LmArgs a) {
@@ -1370,12 +1379,22 @@ lmhead_wide_kernel(LmArgs a) {
   const int r = lane & 15, g = lane >> 4;
   const int ntiles = (a.M + 15) >> 4;
   const int bid = blockIdx.x, nwg = gridDim.x;
-  // a contiguous range of tiles per workgroup (>= 1 tile: the grid has at most ntiles
-  // workgroups), so the four tiles whose logits share a 128-byte line of an output row
-  // are written from one CU
+  // Tiles go out in groups of TG consecutive tiles, group j to workgroup j mod nwg (TG = 0:
+  // one contiguous range per workgroup), so the four tiles whose logits share a 128-byte
+  // line of an output row are written from one CU; the tiles left after the last full round
+  // go out one at a time (at most one more tile than another workgroup; >= 1 tile each: the
+  // grid has at most ntiles workgroups).  Local tile i of a workgroup is global tile
+  // gtile(i), increasing in i.
+  constexpr int TG = WideTileGroup<MODE>::TG;
+  const int full = TG ? ntiles / (TG * nwg) : 0;
+  const int left = ntiles - TG * full * nwg;
   const int tpw = ntiles / nwg, trem = ntiles % nwg;
-  const int my_tiles = tpw + (bid < trem ? 1 : 0);
+  const int my_tiles = TG ? TG * full + (bid < left ? (left - 1 - bid) / nwg + 1 : 0) : tpw + (bid < trem ? 1 : 0);
   const int t0 = bid * tpw + min(bid, trem);
+  auto gtile = [&](int i) {
+    if constexpr (TG == 0) return t0 + i;
+    return i < TG * full ? ((i / TG) * nwg + bid) * TG + (i % TG) : TG * full * nwg + bid + (i - TG * full) * nwg;
+  };
 
   // Prologue: the activations in halves of up to 32 batch rows through the shared staging
   // code (which also quantizes them), each compute wave keeping its fragments in registers.
@@ -1433,7 +1452,7 @@ lmhead_wide_kernel(LmArgs a) {
     for (int s = 0; s < nsteps; ++s) {
       const int i = s - NW;
       if (i >= 0) {
-        const int ctile = t0 + i;
+        const int ctile = gtile(i);
         const bool tile_full = ctile * 16 + 16 <= a.M;
         if (T::ROWSCALE && tile_full) tile_scales_smem<MODE>(a, ctile, sdw);
         Acc<MODE, NCT> acc;
@@ -1487,14 +1506,14 @@ lmhead_wide_kernel(LmArgs a) {
   uint8_t* ring = smem + wave * (S * G::SLOT);
   IssueOffsets<MODE> io;
   const int nst = my_tiles * SPW;
-  int itile = t0, iks = 0, iq = 0;
+  int ltile = 0, itile = gtile(0), iks = 0, iq = 0;
   issue_offsets<MODE>(a, KB, itile, lane, io);
   auto issue_next = [&](uint8_t* slot) {
     issue_stage<MODE>(a, KB, itile, wave * SPW + iks, slot, lane, io);
     ++iq;
     if (++iks == SPW) {
       iks = 0;
-      itile += 1;
+      itile = gtile(++ltile);
       if (iq < nst) issue_offsets<MODE>(a, KB, itile, lane, io);
     }
   };
@@ -1570,10 +1589,10 @@ lmhead_wide_kernel(LmArgs a) {
   __syncthreads();
   const int nh = min(my_tiles, cap), n2 = nreg_lds;
   const bool vec16 = ((uintptr_t)a.out & 15) == 0 && (a.ldo & 7) == 0;
-  auto flush = [&](const uint8_t* src, int rowb, int nt, int tfirst) {
+  auto flush = [&](const uint8_t* src, int rowb, int nt, int lfirst) {
     for (int u = threadIdx.x; u < a.Bg * 2 * nt; u += 64 * (NW + 1)) {
       const int b = u / (2 * nt), p = u - b * (2 * nt);
-      const int r0 = tfirst * 16 + 8 * p;
+      const int r0 = gtile(lfirst + (p >> 1)) * 16 + 8 * (p & 1);
       const v4i v = *(const v4i*)(src + b * rowb + 16 * p);
       uint16_t* op = a.out + (int64_t)b * a.ldo + r0;
       if (vec16 && r0 + 8 <= a.M) {
@@ -1593,8 +1612,8 @@ lmhead_wide_kernel(LmArgs a) {
       }
     }
   };
-  flush(hold, hrow, nh, t0);
-  if (n2 > 0) flush(smem, HROW2, n2, t0 + cap);
+  flush(hold, hrow, nh, 0);
+  if (n2 > 0) flush(smem, HROW2, n2, cap);
 }
 
 // The token of each batch row of a fused lm_head + sampling launch: one wave per row
