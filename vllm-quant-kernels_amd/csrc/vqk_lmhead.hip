@@ -1392,8 +1392,10 @@ lmhead_wide_kernel(LmArgs a) {
   const int my_tiles = TG ? TG * full + (bid < left ? (left - 1 - bid) / nwg + 1 : 0) : tpw + (bid < trem ? 1 : 0);
   const int t0 = bid * tpw + min(bid, trem);
   auto gtile = [&](int i) {
-    if constexpr (TG == 0) return t0 + i;
-    return i < TG * full ? ((i / TG) * nwg + bid) * TG + (i % TG) : TG * full * nwg + bid + (i - TG * full) * nwg;
+    if constexpr (TG == 0)
+      return t0 + i;
+    else
+      return i < TG * full ? ((i / TG) * nwg + bid) * TG + (i % TG) : TG * full * nwg + bid + (i - TG * full) * nwg;
   };
 
   // Prologue: the activations in halves of up to 32 batch rows through the shared staging
