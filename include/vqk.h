@@ -105,9 +105,9 @@ int vqk_act_cast_e4m3(const void *x, int x_dtype, int64_t ldx, int64_t B, int64_
  * Shapes handled: K % 128 == 0 (K % 256 == 0 for MXFP4), M >= 1, 0 <= B <= 2^24 with
  * B * K / 8 < 2^31, row stride of every weight matrix = its logical width (contiguous
  * rows).  Batches larger than one launch's LDS budget are split in groups of up to 32
- * rows (W8A16: 16), launched up to four groups at a time; at K = 3072, 17-64 rows run as
- * one K-split launch (FP8 and MXFP8 from 13 rows; W8A16: 9-32 rows per launch, larger
- * batches in balanced launches of at most 32). */
+ * rows (W8A16: 16), launched up to four groups at a time; at K = 3072, 13-64 rows run as
+ * one K-split launch (W8A16: 9-32 rows per launch, larger batches in balanced launches of
+ * at most 32). */
 
 /* W8A16: out = fp16( f32(s16[m]) * sum_k f32(w[m,k]) * f32(x[b,k]) ).
  * Replaces: int8_gmv (src/vllm_quant_kernels/_kernels.py:8-84) and int8_gemm (:148-250)

@@ -72,15 +72,16 @@ constexpr int LM_WIDE_STAGES = 4;
 // - wide-batch kernel: tiles of logits its writer wave holds in registers beyond those
 //   that wait in LDS;
 constexpr int LM_WIDE_HOLD_REGS = 24;
-constexpr int LM_WIDE_MIN_B = 17;
 // (W8A16 at 248320 x 3072, us per call, row-tiled / wide: B=8 116.2-117.6 / 121.4-121.7
 // (two column tiles), B=9 ~125 / 120.7-120.9 and B=16 123.5-126.1 / 120.3-120.9 (one
 // tile), B=17 205-207 / 124-127)
 constexpr int LM_WIDE_MIN_B_W8A16 = 9;
-// (FP8 and MXFP8 on one column tile, row-tiled / wide: FP8 B=16 123.5-124.9 / 122.2-123.8,
-// B=12 121.3-122.7 / 121.1-122.5, B=9 120.4-121.0 / 121.1-121.5; MXFP8 B=16 124.8-125.6 /
-// 124.4-124.7, B=12 equal, B=9 121.5-122.1 / 122.9-123.1; MXFP4 B=9 68.6 / 70.1)
-constexpr int LM_WIDE_MIN_B_E4M3 = 13;
+// (the other modes on one column tile, row-tiled / wide: FP8 B=16 123.5-124.9 /
+// 122.2-123.8, B=12 121.3-122.7 / 121.1-122.5, B=9 120.4-121.0 / 121.1-121.5; MXFP8 B=16
+// 124.8-125.6 / 124.4-124.7, B=12 equal, B=9 121.5-122.1 / 122.9-123.1; W8A8 B=16
+// 125.9-127.9 / 124.9-126.1, B=13 125.9-126.5 / 124.2-124.7; MXFP4 B=16 70.8-71.5 /
+// 69.5-70.0, B=13 70.1-70.8 / 69.2-69.6, B=9 68.6 / 70.1)
+constexpr int LM_WIDE_MIN_B = 13;
 // (batches above 64 rows, us per call, grouped row-tiled / balanced wide launches: FP8 80
 // 240 / 252, 96 257 / 256, 128 315 / 268, 256 625 / 527; MXFP8 96 278 / 261, 128 342 / 271;
 // W8A8 96 272 / 264, 128 335 / 278; MXFP4 80 176 / 166, 128 214 / 189)
@@ -1691,9 +1692,7 @@ struct WideShape {
   static constexpr int SPW = (MODE == M_MXFP4 || MODE == M_W8A16) ? 2 : 4;
   static constexpr int NW = (MODE == M_W8A16) ? 6 : 3;
   static constexpr int MAXB = (MODE == M_W8A16) ? 32 : 64;
-  static constexpr int MINB = (MODE == M_W8A16)                      ? LM_WIDE_MIN_B_W8A16
-                              : (MODE == M_FP8 || MODE == M_MXFP8) ? LM_WIDE_MIN_B_E4M3
-                                                                   : LM_WIDE_MIN_B;
+  static constexpr int MINB = (MODE == M_W8A16) ? LM_WIDE_MIN_B_W8A16 : LM_WIDE_MIN_B;
   static constexpr int SPLIT_MIN_B = (MODE == M_W8A16 || MODE == M_MXFP4) ? MAXB + 1 : LM_WIDE_SPLIT_MIN_B;
   static bool fits(int KB) { return KB == NW * SPW * 256; }
 };
@@ -1839,8 +1838,8 @@ static int lmhead_launch(const uint8_t* w, const void* ws, const void* x, int xd
         const int Bw = (int)((left + nwl - 1) / nwl);
         a.Bg = Bw;
         a.glast_Bg = Bw;
-        // the kernel's column tiles (up to 16 rows on one tile: W8A16 from 9 rows, FP8 and
-        // MXFP8 from 13; W8A8 and MXFP4 start at 17 rows)
+        // the kernel's column tiles (up to 16 rows on one tile: W8A16 from 9 rows, the other
+        // modes from 13)
         const int nct_w = (Bw <= 16) ? 1 : (Bw <= 32 ? 2 : (Bw + 15) / 16);
         const size_t ring_w = (size_t)W::NW * LM_WIDE_STAGES * G::SLOT;
         const size_t hand_w = (size_t)2 * W::NW * nct_w * 64 * 16;
